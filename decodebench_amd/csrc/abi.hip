@@ -1,0 +1,231 @@
+// abi.hip -- the extern "C" surface of libdecodebench_hip.so.
+//
+// Each entry point checks its whole argument contract first and returns
+// DB_ERR_INVALID without touching the HIP runtime when it is broken, so the
+// checks can be exercised on a host without a GPU.  Only then is the device
+// queried (CU count, cached per device) and the kernel launched on the
+// caller's stream.
+#include <math.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <atomic>
+
+#include "../../include/decodebench_hip.h"
+#include "db_kernels.h"
+
+namespace dbk {
+
+Tuning& tuning() {
+  static Tuning t;
+  return t;
+}
+
+int device_cu_count(int* err) {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    *err = (int)e;
+    return 0;
+  }
+  if (dev >= 0 && dev < 64) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int cus = 0;
+  e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess || cus <= 0) {
+    *err = e != hipSuccess ? (int)e : (int)hipErrorInvalidValue;
+    return 0;
+  }
+  if (dev >= 0 && dev < 64) cache[dev].store(cus, std::memory_order_relaxed);
+  *err = 0;
+  return cus;
+}
+
+int f4_max_splits(int G);
+
+}  // namespace dbk
+
+namespace {
+
+thread_local char g_err[512];
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return DB_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ok();
+  return fail((int)e, "%s: HIP error %d (%s)", what, (int)e, hipGetErrorString(e));
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// LDS budget of one GEMV workgroup for its activation rows (gfx950: 160 KB
+// per CU; keep 8 KB for static arrays).
+constexpr size_t kGemvLdsBudget = 152 * 1024;
+
+int check_gemv(const char* fn, const void* x, const void* W, const void* y,
+               int B, int K, int N, int w_dtype, const void* scale,
+               const void* W2, const void* scale2) {
+  if (!x || !W || !y) return fail(DB_ERR_INVALID, "%s: null tensor pointer", fn);
+  if (B < 1 || N < 1 || K < 8)
+    return fail(DB_ERR_INVALID, "%s: need B >= 1, N >= 1, K >= 8 (got B=%d K=%d N=%d)",
+                fn, B, K, N);
+  if (K % 8 != 0) return fail(DB_ERR_INVALID, "%s: K=%d must be a multiple of 8", fn, K);
+  if ((size_t)K * 16 > kGemvLdsBudget * 8)
+    return fail(DB_ERR_INVALID, "%s: K=%d exceeds the LDS activation budget", fn, K);
+  if (!aligned16(x) || !aligned16(W) || !aligned16(y) || (W2 && !aligned16(W2)))
+    return fail(DB_ERR_INVALID, "%s: tensors must be 16-byte aligned", fn);
+  if (w_dtype == DB_DTYPE_F16) {
+    if (scale || scale2)
+      return fail(DB_ERR_INVALID, "%s: fp16 weights take no scale vector", fn);
+  } else if (w_dtype == DB_DTYPE_FP8_E4M3) {
+    return fail(DB_ERR_UNSUPPORTED, "%s: fp8 e4m3 weights are not implemented yet", fn);
+  } else {
+    return fail(DB_ERR_INVALID, "%s: unknown weight dtype %d", fn, w_dtype);
+  }
+  return DB_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int db_abi_version(void) { return DB_ABI_VERSION; }
+
+const char* db_last_error(void) { return g_err; }
+
+int db_device_cu_count(int* cu_count) {
+  if (!cu_count) return fail(DB_ERR_INVALID, "db_device_cu_count: null output");
+  int err = 0;
+  const int c = dbk::device_cu_count(&err);
+  if (err) return hip_status((hipError_t)err, "db_device_cu_count");
+  *cu_count = c;
+  return ok();
+}
+
+int db_f1_rmsnorm_gemv(const void* x, const void* g, const void* W,
+                       const float* w_scale, void* y, int B, int K, int N,
+                       float eps, int w_dtype, void* stream) {
+  const char* fn = "db_f1_rmsnorm_gemv";
+  if (!g) return fail(DB_ERR_INVALID, "%s: null gain pointer", fn);
+  if (!aligned16(g)) return fail(DB_ERR_INVALID, "%s: tensors must be 16-byte aligned", fn);
+  if (!(eps >= 0.0f) || !isfinite(eps))
+    return fail(DB_ERR_INVALID, "%s: eps must be finite and >= 0", fn);
+  int rc = check_gemv(fn, x, W, y, B, K, N, w_dtype, w_scale, nullptr, nullptr);
+  if (rc) return rc;
+  int err = 0;
+  const int cus = dbk::device_cu_count(&err);
+  if (err) return hip_status((hipError_t)err, fn);
+  return hip_status(dbk::launch_gemv(dbk::kGemvRmsNorm, x, g, W, nullptr, y, B, K,
+                                     N, eps, cus, (hipStream_t)stream),
+                    fn);
+}
+
+int db_f2_gateup_swiglu(const void* x, const void* Wg, const void* Wu,
+                        const float* sg, const float* su, void* y, int B,
+                        int K, int N, int w_dtype, void* stream) {
+  const char* fn = "db_f2_gateup_swiglu";
+  if (!Wu) return fail(DB_ERR_INVALID, "%s: null tensor pointer", fn);
+  int rc = check_gemv(fn, x, Wg, y, B, K, N, w_dtype, sg, Wu, su);
+  if (rc) return rc;
+  int err = 0;
+  const int cus = dbk::device_cu_count(&err);
+  if (err) return hip_status((hipError_t)err, fn);
+  return hip_status(dbk::launch_gemv(dbk::kGemvSwiGLU, x, nullptr, Wg, Wu, y, B,
+                                     K, N, 0.0f, cus, (hipStream_t)stream),
+                    fn);
+}
+
+int db_gemv(const void* x, const void* W, const float* w_scale, void* y, int B,
+            int K, int N, int w_dtype, void* stream) {
+  const char* fn = "db_gemv";
+  int rc = check_gemv(fn, x, W, y, B, K, N, w_dtype, w_scale, nullptr, nullptr);
+  if (rc) return rc;
+  int err = 0;
+  const int cus = dbk::device_cu_count(&err);
+  if (err) return hip_status((hipError_t)err, fn);
+  return hip_status(dbk::launch_gemv(dbk::kGemvPlain, x, nullptr, W, nullptr, y, B,
+                                     K, N, 0.0f, cus, (hipStream_t)stream),
+                    fn);
+}
+
+int db_f4_default_splits(int B, int Hkv, int L, int cu_count) {
+  if (B < 1 || Hkv < 1 || L < 1 || cu_count < 1) return 1;
+  return dbk::f4_choose_splits(B, Hkv, L, cu_count);
+}
+
+size_t db_f4_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S) {
+  if (B < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv || L < 1 || D < 1 || S <= 1) return 0;
+  return dbk::f4_workspace_bytes(B, Hq, Hkv, S, D);
+}
+
+int db_f4_splitkv(const void* q, const void* k, const void* v, void* o,
+                  void* ws, size_t ws_bytes, int B, int Hq, int Hkv, int L,
+                  int D, int S, float scale, void* stream) {
+  const char* fn = "db_f4_splitkv";
+  if (!q || !k || !v || !o) return fail(DB_ERR_INVALID, "%s: null tensor pointer", fn);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+    return fail(DB_ERR_INVALID, "%s: tensors must be 16-byte aligned", fn);
+  if (B < 1 || Hq < 1 || Hkv < 1 || L < 1)
+    return fail(DB_ERR_INVALID, "%s: need B, Hq, Hkv, L >= 1 (got %d %d %d %d)", fn, B,
+                Hq, Hkv, L);
+  if (D != 128) return fail(DB_ERR_INVALID, "%s: head_dim D=%d, only 128 is supported", fn, D);
+  if (Hq % Hkv != 0)
+    return fail(DB_ERR_INVALID, "%s: Hq=%d is not a multiple of Hkv=%d", fn, Hq, Hkv);
+  const int G = Hq / Hkv;
+  if (G != 1 && G != 2 && G != 4 && G != 8)
+    return fail(DB_ERR_INVALID, "%s: query heads per KV head G=%d not in {1,2,4,8}", fn, G);
+  if (S < 1 || S > 256 || S > dbk::f4_max_splits(G))
+    return fail(DB_ERR_INVALID, "%s: split count S=%d outside [1, 256]", fn, S);
+  if (!isfinite(scale)) return fail(DB_ERR_INVALID, "%s: scale must be finite", fn);
+  if ((size_t)B * Hkv * L * D >= ((size_t)1 << 40))
+    return fail(DB_ERR_INVALID, "%s: KV cache too large", fn);
+  const int ntiles = (L + 15) / 16;
+  const int s_eff = S < ntiles ? S : ntiles;
+  if (s_eff > 1) {
+    const size_t need = dbk::f4_workspace_bytes(B, Hq, Hkv, S, D);
+    if (!ws) return fail(DB_ERR_INVALID, "%s: S=%d needs a workspace", fn, S);
+    if (!aligned16(ws)) return fail(DB_ERR_INVALID, "%s: workspace must be 16-byte aligned", fn);
+    if (ws_bytes < need)
+      return fail(DB_ERR_INVALID, "%s: workspace %zu bytes < %zu required", fn, ws_bytes,
+                  need);
+  }
+  return hip_status(dbk::launch_f4(q, k, v, o, ws, B, Hq, Hkv, L, D, S, scale,
+                                   (hipStream_t)stream),
+                    fn);
+}
+
+int db_tune(const char* key, int value) {
+  if (!key) return fail(DB_ERR_INVALID, "db_tune: null key");
+  dbk::Tuning& t = dbk::tuning();
+  if (!strcmp(key, "gemv_waves_per_cu")) {
+    t.gemv_waves_per_cu = value > 0 ? value : 0;
+  } else if (!strcmp(key, "f4_blocks_per_cu")) {
+    if (value < 1) return fail(DB_ERR_INVALID, "db_tune: f4_blocks_per_cu must be >= 1");
+    t.f4_blocks_per_cu = value;
+  } else if (!strcmp(key, "f4_min_tiles")) {
+    if (value < 1) return fail(DB_ERR_INVALID, "db_tune: f4_min_tiles must be >= 1");
+    t.f4_min_tiles = value;
+  } else {
+    return fail(DB_ERR_INVALID, "db_tune: unknown key '%s'", key);
+  }
+  return ok();
+}
+
+}  // extern "C"

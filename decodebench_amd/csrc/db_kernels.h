@@ -1,0 +1,38 @@
+// db_kernels.h -- host-side launchers shared by the kernel files and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+namespace dbk {
+
+// Launch geometry knobs; defaults are the tuned MI355X values.  They can be
+// changed at run time through db_tune() for launch-shape sweeps.
+struct Tuning {
+  int gemv_waves_per_cu = 0;   // 0: choose from the row-group count
+  int f4_blocks_per_cu = 2;    // target resident F4 blocks per CU
+  int f4_min_tiles = 2;        // minimum 16-row tiles per F4 block
+};
+Tuning& tuning();
+
+// Compute units of the current device (cached per device ordinal).
+int device_cu_count(int* err);
+
+enum GemvMode : int { kGemvPlain = 0, kGemvRmsNorm = 1, kGemvSwiGLU = 2 };
+
+// y[B,N] = op(x[B,K]) . W^T  (fp16 in/out, fp32 accumulation).
+//   kGemvPlain   : y = x W^T
+//   kGemvRmsNorm : y = fp16(fp16(x * rsqrt(mean(x^2) + eps)) * gamma) W^T
+//   kGemvSwiGLU  : y = fp16(silu(fp16(x Wg^T)) * fp16(x Wu^T))
+hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
+                       const void* w0, const void* w1, void* y, int B, int K,
+                       int N, float eps, int cu_count, hipStream_t stream);
+
+// Split-KV GQA decode attention with the log-sum-exp combine in-kernel.
+size_t f4_workspace_bytes(int B, int Hq, int Hkv, int S, int D);
+int f4_choose_splits(int B, int Hkv, int L, int cu_count);
+hipError_t launch_f4(const void* q, const void* k, const void* v, void* o,
+                     void* ws, int B, int Hq, int Hkv, int L, int D, int S,
+                     float scale, hipStream_t stream);
+
+}  // namespace dbk

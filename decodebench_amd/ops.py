@@ -1,0 +1,273 @@
+"""Fused decode ops backed by libdecodebench_hip.so (HIP, gfx950).
+
+Each op takes torch tensors on the GPU, allocates its output with
+``torch.empty`` and launches one kernel on ``torch.cuda.current_stream()``
+through the C ABI declared in ``include/decodebench_hip.h``.  No op allocates
+inside the library, synchronises, or reads device memory on the host, so the
+ops work as ``Sequence`` stages, inside a ``profile(fused=...)`` callable, and
+under ``torch.cuda.graph`` capture.
+
+This follows the plug-in pattern of the reference's custom-kernel example
+(examples/custom_kernel/bindings.cpp:13-30: output from ``empty_like``, launch
+on the current stream) with ctypes over a C ABI instead of a torch extension.
+
+There is no fallback: if the HIP library is missing or cannot be loaded the
+ops raise ``RuntimeError`` naming the build command.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import math
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libdecodebench_hip.so"
+
+DB_OK = 0
+DB_ERR_INVALID = -1
+DB_ERR_UNSUPPORTED = -2
+DTYPE_F16 = 0
+DTYPE_FP8_E4M3 = 1
+
+_lock = threading.Lock()
+_lib = None
+_cu_cache: dict[int, int] = {}
+_ws_cache: dict[tuple, object] = {}
+
+_p = C.c_void_p
+_i = C.c_int
+
+
+def load_library():
+    """Load the HIP library (after torch, so both share one HIP runtime)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        import torch  # noqa: F401  -- torch's libamdhip64 must be loaded first
+
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"HIP library {LIB_PATH} is not built; run "
+                "`python -m decodebench_amd.build` (hipcc, gfx950)")
+        lib = C.CDLL(str(LIB_PATH))
+        protos = {
+            "db_abi_version": (_i, []),
+            "db_last_error": (C.c_char_p, []),
+            "db_device_cu_count": (_i, [C.POINTER(_i)]),
+            "db_f1_rmsnorm_gemv": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, C.c_float, _i, _p]),
+            "db_f2_gateup_swiglu": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p]),
+            "db_gemv": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p]),
+            "db_f4_default_splits": (_i, [_i, _i, _i, _i]),
+            "db_f4_workspace_bytes": (C.c_size_t, [_i, _i, _i, _i, _i, _i]),
+            "db_f4_splitkv": (_i, [_p, _p, _p, _p, _p, C.c_size_t, _i, _i, _i, _i, _i, _i,
+                                   C.c_float, _p]),
+            "db_tune": (_i, [C.c_char_p, _i]),
+        }
+        for name, (res, args) in protos.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        if lib.db_abi_version() != 1:
+            raise RuntimeError("libdecodebench_hip.so ABI version mismatch")
+        _lib = lib
+        return lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc == DB_OK:
+        return
+    msg = load_library().db_last_error().decode(errors="replace")
+    if rc == DB_ERR_INVALID:
+        raise ValueError(f"{what}: {msg}")
+    if rc == DB_ERR_UNSUPPORTED:
+        raise NotImplementedError(f"{what}: {msg}")
+    raise RuntimeError(f"{what} failed (HIP error {rc}): {msg}")
+
+
+def _stream_ptr(t) -> int:
+    import torch
+
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _require(t, name: str, dtype=None) -> None:
+    import torch
+
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on a GPU device (got {t.device})")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype} (got {t.dtype})")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def cu_count(device=None) -> int:
+    import torch
+
+    dev = torch.device("cuda" if device is None else device)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    if idx not in _cu_cache:
+        _cu_cache[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return _cu_cache[idx]
+
+
+def tune(key: str, value: int) -> None:
+    """Set a launch-geometry knob of the library (for tuning sweeps)."""
+    _check(load_library().db_tune(key.encode(), int(value)), "db_tune")
+
+
+def _weights(W, w_scale, name: str, N: int, K: int):
+    """(dtype code, scale pointer) for an fp16 or e4m3 weight matrix."""
+    import torch
+
+    if W.dtype == torch.float16:
+        if w_scale is not None:
+            raise ValueError(f"{name}: fp16 weights take no scale")
+        return DTYPE_F16, None
+    if W.dtype in (torch.float8_e4m3fn, torch.uint8):
+        if w_scale is None:
+            raise ValueError(f"{name}: fp8 weights need a per-row fp32 scale")
+        _require(w_scale, f"{name} scale", torch.float32)
+        if tuple(w_scale.shape) != (N,):
+            raise ValueError(f"{name} scale must have shape ({N},)")
+        return DTYPE_FP8_E4M3, w_scale.data_ptr()
+    raise TypeError(f"{name}: unsupported weight dtype {W.dtype}")
+
+
+def _as_2d(x, name: str):
+    if x.dim() == 1:
+        return x.unsqueeze(0), True
+    if x.dim() != 2:
+        raise ValueError(f"{name} must be [K] or [B, K] (got {tuple(x.shape)})")
+    return x, False
+
+
+def f1_rmsnorm_gemv(x, g, W, eps: float = 1e-6, w_scale=None):
+    """F1: ``F.linear(rmsnorm(x, g, eps), W)`` in one kernel.
+
+    x [B,K] (or [K]) fp16, g [K] fp16, W [N,K] fp16 (or e4m3 + w_scale [N]).
+    Returns [B,N] fp16 (or [N] for a 1-D x)."""
+    import torch
+
+    _require(x, "x", torch.float16)
+    _require(g, "g", torch.float16)
+    _require(W, "W")
+    x2, squeeze = _as_2d(x, "x")
+    B, K = x2.shape
+    if W.dim() != 2 or W.shape[1] != K or g.shape != (K,):
+        raise ValueError(f"shape mismatch: x {tuple(x.shape)}, g {tuple(g.shape)}, "
+                         f"W {tuple(W.shape)}")
+    N = W.shape[0]
+    dt, sp = _weights(W, w_scale, "W", N, K)
+    y = torch.empty((B, N), dtype=torch.float16, device=x.device)
+    rc = load_library().db_f1_rmsnorm_gemv(x2.data_ptr(), g.data_ptr(), W.data_ptr(), sp,
+                                           y.data_ptr(), B, K, N, float(eps), dt,
+                                           _stream_ptr(x))
+    _check(rc, "db_f1_rmsnorm_gemv")
+    return y[0] if squeeze else y
+
+
+def f2_gateup_swiglu(x, Wg, Wu, sg=None, su=None):
+    """F2: ``silu(F.linear(x, Wg)) * F.linear(x, Wu)`` in one kernel.
+
+    x [B,K] (or [K]) fp16, Wg/Wu [N,K] fp16 (or e4m3 + per-row scales)."""
+    import torch
+
+    _require(x, "x", torch.float16)
+    _require(Wg, "Wg")
+    _require(Wu, "Wu")
+    x2, squeeze = _as_2d(x, "x")
+    B, K = x2.shape
+    if Wg.dim() != 2 or Wg.shape != Wu.shape or Wg.shape[1] != K or Wg.dtype != Wu.dtype:
+        raise ValueError(f"shape mismatch: x {tuple(x.shape)}, Wg {tuple(Wg.shape)}, "
+                         f"Wu {tuple(Wu.shape)}")
+    N = Wg.shape[0]
+    dt, sgp = _weights(Wg, sg, "Wg", N, K)
+    _, sup = _weights(Wu, su, "Wu", N, K)
+    y = torch.empty((B, N), dtype=torch.float16, device=x.device)
+    rc = load_library().db_f2_gateup_swiglu(x2.data_ptr(), Wg.data_ptr(), Wu.data_ptr(),
+                                            sgp, sup, y.data_ptr(), B, K, N, dt,
+                                            _stream_ptr(x))
+    _check(rc, "db_f2_gateup_swiglu")
+    return y[0] if squeeze else y
+
+
+def gemv(x, W, w_scale=None):
+    """Plain projection ``F.linear(x, W)`` (fp16 out, fp32 accumulation)."""
+    import torch
+
+    _require(x, "x", torch.float16)
+    _require(W, "W")
+    x2, squeeze = _as_2d(x, "x")
+    B, K = x2.shape
+    if W.dim() != 2 or W.shape[1] != K:
+        raise ValueError(f"shape mismatch: x {tuple(x.shape)}, W {tuple(W.shape)}")
+    N = W.shape[0]
+    dt, sp = _weights(W, w_scale, "W", N, K)
+    y = torch.empty((B, N), dtype=torch.float16, device=x.device)
+    rc = load_library().db_gemv(x2.data_ptr(), W.data_ptr(), sp, y.data_ptr(), B, K, N, dt,
+                                _stream_ptr(x))
+    _check(rc, "db_gemv")
+    return y[0] if squeeze else y
+
+
+def f4_default_splits(B: int, Hkv: int, L: int, device=None) -> int:
+    return int(load_library().db_f4_default_splits(B, Hkv, L, cu_count(device)))
+
+
+def f4_workspace(B: int, Hq: int, Hkv: int, L: int, D: int, S: int, device):
+    """Zero-filled workspace for db_f4_splitkv, cached per shape and device.
+
+    The kernel re-arms the workspace after every call, so one cached buffer
+    serves every later call with the same shape on that device (calls on that
+    buffer must not overlap in time)."""
+    import torch
+
+    nbytes = int(load_library().db_f4_workspace_bytes(B, Hq, Hkv, L, D, S))
+    if nbytes == 0:
+        return None
+    dev = torch.device(device)
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), nbytes)
+    ws = _ws_cache.get(key)
+    if ws is None:
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        _ws_cache[key] = ws
+    return ws
+
+
+def f4_flashdecode(q, K, V, scale: float | None = None, n_splits: int | None = None,
+                   workspace=None):
+    """F4: split-KV GQA decode attention with the LSE combine, one launch.
+
+    q [B,Hq,D], K/V [B,Hkv,L,D] fp16 (D = 128); query head h reads KV head
+    h // (Hq // Hkv).  ``scale`` defaults to 1/sqrt(D); ``n_splits`` defaults
+    to the library's CU-count-based choice.  Returns [B,Hq,D] fp16."""
+    import torch
+
+    for t, n in ((q, "q"), (K, "K"), (V, "V")):
+        _require(t, n, torch.float16)
+    if q.dim() != 3 or K.dim() != 4 or K.shape != V.shape:
+        raise ValueError(f"expected q [B,Hq,D] and K, V [B,Hkv,L,D]; got q {tuple(q.shape)}, "
+                         f"K {tuple(K.shape)}, V {tuple(V.shape)}")
+    B, Hq, D = q.shape
+    Bk, Hkv, L, Dk = K.shape
+    if Bk != B or Dk != D:
+        raise ValueError(f"q {tuple(q.shape)} and K {tuple(K.shape)} disagree on B or D")
+    scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    S = f4_default_splits(B, Hkv, L, q.device) if n_splits is None else int(n_splits)
+    if workspace is None:
+        workspace = f4_workspace(B, Hq, Hkv, L, D, S, q.device)
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    o = torch.empty((B, Hq, D), dtype=torch.float16, device=q.device)
+    rc = load_library().db_f4_splitkv(q.data_ptr(), K.data_ptr(), V.data_ptr(), o.data_ptr(),
+                                      ws_ptr, ws_bytes, B, Hq, Hkv, L, D, S, scale,
+                                      _stream_ptr(q))
+    _check(rc, "db_f4_splitkv")
+    return o

@@ -1,0 +1,128 @@
+/* decodebench_hip.h -- C ABI of libdecodebench_hip.so (MI355X / gfx950).
+ *
+ * The fused decode hot path of DecodeBench behind plain C entry points:
+ * pointers, sizes and a HIP stream handle, no C++ or torch types.  Every
+ * tensor is dense, row-major and 16-byte aligned; fp16 data is IEEE binary16.
+ *
+ * Conventions shared by every entry point
+ *  - Return value: DB_OK (0) on success; DB_ERR_INVALID (-1) when an argument
+ *    breaks the contract (checked before any HIP call, so it also works on a
+ *    machine without a GPU); DB_ERR_UNSUPPORTED (-2) for a valid but not yet
+ *    implemented combination; a positive value is the hipError_t the HIP
+ *    runtime reported for the launch.  db_last_error() describes the last
+ *    non-zero return on the calling thread.
+ *  - The library never allocates, frees or synchronises and never reads
+ *    device memory on the host; the caller owns every buffer, including the
+ *    F4 workspace.  Kernels are launched only on `stream` (NULL = the legacy
+ *    default stream), so a call can be captured into a hipGraph.
+ *  - Calls are reentrant; two calls that share an F4 workspace must not
+ *    overlap in time.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository
+ * animeshsri14/Decodebench):
+ *  - the fused CUDA kernels f1_kernel / f2_kernel / f4_partial_kernel +
+ *    f4_reduce_kernel, each taking the by-value parameter block KernelArgs
+ *    (validation/include/decodebench_val/kernel_args.h:24-103), with launch
+ *    geometry chosen by the native harness
+ *    (validation/src/bench/bench_variant.cu:376-387, 558-565, 714-719, 753-763);
+ *  - the torch-extension FFI pattern the reference documents for plugging a
+ *    kernel into Sequence stages and Sequence.profile(fused=...)
+ *    (examples/custom_kernel/bindings.cpp:13-30, kernel.cu:60-73).
+ */
+#ifndef DECODEBENCH_HIP_H
+#define DECODEBENCH_HIP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DB_ABI_VERSION 1
+
+#define DB_OK 0
+#define DB_ERR_INVALID (-1)
+#define DB_ERR_UNSUPPORTED (-2)
+
+/* Weight element types accepted by the GEMV entry points. */
+#define DB_DTYPE_F16 0
+#define DB_DTYPE_FP8_E4M3 1 /* OCP e4m3fn + per-output-row fp32 scale */
+
+/* ABI revision of this header (DB_ABI_VERSION). */
+int db_abi_version(void);
+
+/* Message for the last non-zero return on this thread ("" if none). */
+const char* db_last_error(void);
+
+/* Compute units of the current HIP device (the F4 split policy uses it). */
+int db_device_cu_count(int* cu_count);
+
+/* F1: y[B,N] = fp16( xh[B,K] . W[N,K]^T ), where
+ *       xh = fp16( fp16( x * rsqrt(mean(x^2, -1) + eps) ) * g )
+ *     with the statistic in fp32 and the GEMV accumulated in fp32.
+ * Replaces f1_kernel(KernelArgs) (validation/src/kernels/fused/f1.cu:18-84)
+ * and the reference stages rmsnorm + gemv
+ * (src/decodebench/demos/llama_decode.py:36-43).
+ * Contract: B >= 1, N >= 1, K >= 8 and K % 8 == 0; x [B,K], g [K], W [N,K],
+ * y [B,N] fp16.  w_dtype must be DB_DTYPE_F16 (w_scale NULL) or
+ * DB_DTYPE_FP8_E4M3 (w_scale [N] fp32, W holds N*K bytes). */
+int db_f1_rmsnorm_gemv(const void* x, const void* g, const void* W,
+                       const float* w_scale, void* y, int B, int K, int N,
+                       float eps, int w_dtype, void* stream);
+
+/* F2: y[B,N] = fp16( fp16(silu(fp16(x Wg^T))) * fp16(x Wu^T) ), fp32
+ * accumulation; the gate and up projections never leave registers.
+ * Replaces f2_kernel(KernelArgs) (validation/src/kernels/fused/f2.cu:17-76)
+ * and the reference stages gate, up, swiglu
+ * (src/decodebench/demos/llama_decode.py:77-87).
+ * Contract as db_f1_rmsnorm_gemv; sg/su are the per-row scales of Wg/Wu
+ * when w_dtype is DB_DTYPE_FP8_E4M3, else NULL. */
+int db_f2_gateup_swiglu(const void* x, const void* Wg, const void* Wu,
+                        const float* sg, const float* su, void* y, int B,
+                        int K, int N, int w_dtype, void* stream);
+
+/* Plain GEMV y[B,N] = fp16( x[B,K] . W[N,K]^T ) with fp32 accumulation: the
+ * unfused projection of the decode-layer chain (O and down projections).
+ * Replaces gemv_kernel(KernelArgs) (validation/src/kernels/unfused/gemv.cu:15-48)
+ * and the reference stage gemv (src/decodebench/demos/llama_decode.py:41-43).
+ * Contract as db_f1_rmsnorm_gemv. */
+int db_gemv(const void* x, const void* W, const float* w_scale, void* y,
+            int B, int K, int N, int w_dtype, void* stream);
+
+/* Split count the library picks for F4 when the caller has no preference:
+ * enough (batch, kv-head, split) workgroups to fill `cu_count` CUs while every
+ * split keeps at least two 16-row tiles.  Replaces the fixed L/128 default and
+ * DECODEBENCH_F4_SPLITS override of the reference harness
+ * (validation/src/bench/bench_variant.cu:714-719). */
+int db_f4_default_splits(int B, int Hkv, int L, int cu_count);
+
+/* Bytes of caller-owned workspace db_f4_splitkv needs for S splits (0 when
+ * S == 1).  The workspace must be zero-filled before its first use; the
+ * kernel leaves it re-armed (its counters back at zero) after every call. */
+size_t db_f4_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S);
+
+/* F4: o[b,h,:] = softmax(scale * q[b,h,:] . K[b,h/G,:,:]^T) . V[b,h/G,:,:]
+ * for G = Hq / Hkv query heads per KV head (grouped-query attention), fp32
+ * softmax and accumulation, fp16 output.  The KV length is cut into S splits
+ * whose partial (max, exp-sum, unnormalised output) records are merged by
+ * log-sum-exp inside the same launch.
+ * Replaces f4_partial_kernel + f4_reduce_kernel
+ * (validation/src/kernels/fused/f4.cu:173-319) and the reference stages
+ * scores, softmax, weighted_v (src/decodebench/demos/llama_decode.py:120-134).
+ * Contract: q [B,Hq,D], K and V [B,Hkv,L,D], o [B,Hq,D] fp16; D == 128;
+ * Hq % Hkv == 0 with G in {1,2,4,8}; L >= 1; 1 <= S <= 256; ws holds at least
+ * db_f4_workspace_bytes(B,Hq,Hkv,L,D,S) bytes (ignored when S == 1). */
+int db_f4_splitkv(const void* q, const void* k, const void* v, void* o,
+                  void* ws, size_t ws_bytes, int B, int Hq, int Hkv, int L,
+                  int D, int S, float scale, void* stream);
+
+/* Launch-geometry knobs for tuning sweeps ("gemv_waves_per_cu",
+ * "f4_blocks_per_cu", "f4_min_tiles"); value <= 0 restores the default for
+ * the GEMV knob.  No counterpart in the reference. */
+int db_tune(const char* key, int value);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DECODEBENCH_HIP_H */

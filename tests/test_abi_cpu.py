@@ -1,0 +1,124 @@
+"""C ABI checks that need no GPU.
+
+* libdecodebench_hip.so loads and exports every function declared in
+  include/decodebench_hip.h;
+* every contract violation returns DB_ERR_INVALID with a message before any
+  HIP call (so these run on a GPU-less host);
+* the Python wrappers turn those codes into ValueError / NotImplementedError.
+"""
+
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "decodebench_hip.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from decodebench_amd import build, ops
+
+    if not ops.LIB_PATH.exists():
+        build.build(verbose=False)
+    return ops.load_library()
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(db_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    names = declared_functions()
+    for want in ("db_abi_version", "db_last_error", "db_f1_rmsnorm_gemv",
+                 "db_f2_gateup_swiglu", "db_gemv", "db_f4_splitkv",
+                 "db_f4_workspace_bytes", "db_f4_default_splits", "db_device_cu_count",
+                 "db_tune"):
+        assert want in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.db_abi_version() == 1
+
+
+P = 0x10000  # a fake, 16-byte aligned device address: never dereferenced
+
+
+def last(lib):
+    return lib.db_last_error().decode()
+
+
+def test_f1_contract_errors(lib):
+    f = lib.db_f1_rmsnorm_gemv
+    assert f(None, P, P, None, P, 1, 4096, 4096, 1e-6, 0, None) == -1
+    assert "null" in last(lib)
+    assert f(P, P, P, None, P, 1, 4100, 4096, 1e-6, 0, None) == -1
+    assert "multiple of 8" in last(lib)
+    assert f(P, P, P, None, P, 0, 4096, 4096, 1e-6, 0, None) == -1
+    assert f(P, P, P + 2, None, P, 1, 4096, 4096, 1e-6, 0, None) == -1
+    assert "aligned" in last(lib)
+    assert f(P, P, P, None, P, 1, 4096, 4096, -1.0, 0, None) == -1
+    assert "eps" in last(lib)
+    assert f(P, P, P, None, P, 1, 4096, 4096, 1e-6, 7, None) == -1
+    assert "dtype" in last(lib)
+    assert f(P, P, P, None, P, 1, 1 << 20, 4096, 1e-6, 0, None) == -1
+    assert "LDS" in last(lib)
+
+
+def test_f2_and_gemv_contract_errors(lib):
+    assert lib.db_f2_gateup_swiglu(P, P, None, None, None, P, 1, 4096, 14336, 0, None) == -1
+    assert lib.db_f2_gateup_swiglu(P, P, P, C.c_void_p(P), None, P, 1, 4096, 14336, 0,
+                                   None) == -1
+    assert "no scale" in last(lib)
+    assert lib.db_gemv(P, P, None, P, 1, 12, 16, 0, None) == -1
+
+
+def test_f4_contract_errors(lib):
+    f = lib.db_f4_splitkv
+    ok = dict(B=1, Hq=32, Hkv=8, L=1024, D=128, S=4)
+
+    def call(ws=P, ws_bytes=1 << 30, **kw):
+        a = {**ok, **kw}
+        return f(P, P, P, P, ws, ws_bytes, a["B"], a["Hq"], a["Hkv"], a["L"], a["D"], a["S"],
+                 0.088, None)
+
+    assert call(D=64) == -1 and "128" in last(lib)
+    assert call(Hq=30) == -1 and "multiple" in last(lib)
+    assert call(Hq=48, Hkv=4) == -1 and "G=12" in last(lib)
+    assert call(L=0) == -1
+    assert call(S=0) == -1 and call(S=257) == -1
+    assert call(ws=None) == -1 and "workspace" in last(lib)
+    assert call(ws_bytes=16) == -1 and "required" in last(lib)
+    assert f(None, P, P, P, P, 1 << 30, 1, 32, 8, 1024, 128, 4, 0.1, None) == -1
+
+
+def test_f4_workspace_and_split_policy(lib):
+    assert lib.db_f4_workspace_bytes(1, 32, 8, 8192, 128, 1) == 0
+    ws = lib.db_f4_workspace_bytes(1, 32, 8, 8192, 128, 64)
+    assert ws >= 8 * 64 * 4 * 130 * 4
+    s = lib.db_f4_default_splits(1, 8, 8192, 256)
+    assert 1 <= s <= 256
+    assert lib.db_f4_default_splits(1, 8, 16, 256) == 1       # one tile -> one split
+    assert lib.db_f4_default_splits(8, 8, 32768, 256) >= 1
+
+
+def test_tune_keys(lib):
+    assert lib.db_tune(b"nope", 1) == -1
+    assert lib.db_tune(b"f4_blocks_per_cu", 0) == -1
+    assert lib.db_tune(b"f4_blocks_per_cu", 2) == 0
+
+
+def test_python_wrappers_raise_on_cpu_tensors():
+    torch = pytest.importorskip("torch")
+    from decodebench_amd import ops
+
+    x = torch.zeros(1, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="GPU"):
+        ops.f1_rmsnorm_gemv(x, torch.zeros(64, dtype=torch.float16),
+                            torch.zeros(8, 64, dtype=torch.float16))
