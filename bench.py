@@ -1,0 +1,287 @@
+"""Benchmark of the fused decode hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+
+Prints ONE JSON line.  The headline workload is BASELINE config 2 at batch 1:
+F2 = gate/up GEMV + SwiGLU, x[1,4096] fp16, Wg/Wu[14336,4096] fp16 ~N(0,0.02).
+A step is one fused launch over a fresh weight replica; the replicas rotate
+through a working set larger than twice the on-die caches (8 x 4 MB L2 plus
+the 256 MB Infinity Cache), so every step streams its weights from HBM.
+
+  value          algorithmic bytes / (timed region / K), GB/s
+  roofline       the F2 kernel against the 8 TB/s HBM3E peak; its average
+                 launch duration is the same event-timed region on the
+                 stream the kernel runs on (torch's current stream)
+  kernels        F1 (config 1 and the QKV shape of config 3) and F4
+                 (config 4 at L = 1024 / 8192 / 32768) at batch 1, each timed
+                 as back-to-back launches replayed from a hipGraph
+  decomposition  Sequence.profile of the unfused torch stages (stream and
+                 graph) against the fused kernel: Delta_launch and B
+  cpu_baseline   the torch CPU restatement of the reference stages
+                 (oracle/stages.py) on this host's cores, F2 at full size
+
+``--gpus N`` with N > 1 exits with an error: this build runs on one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = ("fused kernel µs + HBM GB/s (% of ~8 TB/s) for F1/F2/F4 at bs=1; "
+          "Δ_launch vs B")
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse_args(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--quick", action="store_true",
+                    help="headline only: skip the per-kernel table, the "
+                         "decomposition and the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="bound on the CPU baseline sample")
+    ap.add_argument("--trials", type=int, default=12,
+                    help="trials per variant in the decomposition")
+    return ap.parse_args(argv)
+
+
+# ----------------------------------------------------------------- timing
+def time_steps(case, steps: int, warmup: int):
+    """Eager launches, one per step, replica i % n; returns seconds."""
+    import torch
+
+    reps = case.replicas
+    n = len(reps)
+    for i in range(warmup):
+        case.fused(reps[i % n])
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        case.fused(reps[i % n])
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3
+
+
+def time_graph_launches(case, min_launches: int = 96, replays: int = 20):
+    """Per-launch microseconds of the fused kernel, back-to-back in a graph.
+
+    One graph holds whole rotations over the replicas, so the host never
+    throttles the launch rate; returns the median over ``replays``."""
+    import torch
+
+    reps = case.replicas
+    n = len(reps)
+    per_graph = n * max(1, math.ceil(min_launches / n))
+    for r in reps:                       # allocations (F4 workspace) happen here
+        case.fused(r)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(n):
+            case.fused(reps[i])
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(per_graph):
+            case.fused(reps[i % n])
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    samples = []
+    for _ in range(replays):
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        samples.append(e0.elapsed_time(e1) * 1e3 / per_graph)
+    samples.sort()
+    del graph
+    return samples[len(samples) // 2], per_graph
+
+
+def check_case(case) -> float:
+    """Fused output vs the unfused torch stages on the GPU (rtol/atol 1e-2)."""
+    import torch
+
+    ref = case.seq._replay_body(case.inputs).float()
+    out = case.fused(case.inputs).float()
+    torch.cuda.synchronize()
+    if not torch.allclose(out, ref, rtol=1e-2, atol=1e-2):
+        raise RuntimeError(f"{case.name}: fused output differs from the torch stages "
+                           f"(max abs {float((out - ref).abs().max()):.3e})")
+    return float((out - ref).norm() / ref.norm().clamp_min(1e-30))
+
+
+def kernel_row(case, us: float) -> dict:
+    gbs = case.algorithmic_bytes / (us * 1e-6) / 1e9
+    return {"us": round(us, 3), "GB/s": round(gbs, 1),
+            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes": case.algorithmic_bytes,
+            "replicas": len(case.replicas), "shape": case.shape}
+
+
+# ------------------------------------------------------------ CPU baseline
+def cpu_baseline(seconds: float) -> dict:
+    """F2 (config 2, B = 1) through the torch CPU stages, time-bounded."""
+    import torch
+
+    from oracle import stages
+
+    gen = torch.Generator().manual_seed(42)
+    K, N = 4096, 14336
+    x = torch.randn(1, K, generator=gen).half()
+    Wg = (torch.randn(N, K, generator=gen) * 0.02).half()
+    Wu = (torch.randn(N, K, generator=gen) * 0.02).half()
+    nbytes = 2 * N * K * 2 + (K + N) * 2
+    stages.f2(x, Wg, Wu)  # warm-up
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        stages.f2(x, Wg, Wu)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    cpu_model = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"F2 B=1 Wg/Wu[14336,4096] fp16 via oracle/stages.py (torch CPU), "
+                       f"{len(times)} calls in ~{seconds:.0f} s, median "
+                       f"{med * 1e6:.0f} us/call"),
+            "us_per_call": round(med * 1e6, 1), "cpu_model": cpu_model,
+            "os_cpu_count": os.cpu_count()}
+
+
+# -------------------------------------------------------------------- main
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build measures one GPU only (the fused decode kernels run "
+              "on a single MI355X; no multi-GPU path exists). Run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+    if args.steps < 1 or args.warmup < 0:
+        print("bench.py: --steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from decodebench_amd import ops
+    from decodebench_amd.demos.llama_decode import build_config
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    ops.load_library()
+    dev_name = torch.cuda.get_device_name(0)
+    log(f"device {dev_name}, {ops.cu_count()} CUs")
+
+    # ---- headline: F2, config 2, batch 1 --------------------------------
+    head = build_config("f2", batch=1)
+    err = check_case(head)
+    log(f"f2 parity vs torch stages ok (rel-L2 {err:.2e}); {len(head.replicas)} replicas")
+    secs = time_steps(head, args.steps, args.warmup)
+    us = secs * 1e6 / args.steps
+    gbs = head.algorithmic_bytes * args.steps / secs / 1e9
+    log(f"f2 headline: {us:.2f} us/step, {gbs:.1f} GB/s")
+
+    out = {
+        "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(us / 1e3, 6), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic (seeded torch.Generator(42), fp32 -> fp16)",
+        "config": {"workload": "F2 gate/up GEMV + SwiGLU fused, batch 1, x[1,4096], "
+                               "Wg/Wu[14336,4096] fp16 (BASELINE configs[1])",
+                   "batch": 1, "K": 4096, "N": 14336,
+                   "weight_replicas": len(head.replicas), "device": dev_name},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "gemv_kernel<2,...> (F2 SwiGLU mode)",
+                     "algorithmic_bytes_per_launch": head.algorithmic_bytes,
+                     "avg_launch_us": round(us, 3)},
+    }
+    del head
+    torch.cuda.empty_cache()
+
+    if not args.quick:
+        # ---- per-kernel table (graph-replayed back-to-back launches) -----
+        kernels = {}
+        for name, kw in (("f1_cfg1", dict(name="f1")), ("f1_qkv_cfg3", dict(name="f1_qkv")),
+                         ("f2_cfg2", dict(name="f2")),
+                         ("f4_L1024", dict(name="f4", L=1024)),
+                         ("f4_L8192", dict(name="f4", L=8192)),
+                         ("f4_L32768", dict(name="f4", L=32768))):
+            case = build_config(batch=1, **kw)
+            check_case(case)
+            us_k, launches = time_graph_launches(case)
+            kernels[name] = kernel_row(case, us_k)
+            kernels[name]["launches_per_graph"] = launches
+            log(f"{name}: {us_k:.2f} us, {kernels[name]['GB/s']:.0f} GB/s")
+            del case
+            torch.cuda.empty_cache()
+        out["kernels"] = kernels
+
+        # ---- Delta_launch vs B: unfused stream / graph vs fused ----------
+        decomp = {}
+        for name, kw in (("f1_cfg1", dict(name="f1")), ("f2_cfg2", dict(name="f2")),
+                         ("f4_L8192", dict(name="f4", L=8192))):
+            case = build_config(batch=1, **kw)
+            rep = case.seq.profile(case.inputs, trials=args.trials, target_ms=10.0,
+                                   warmup=10, input_replicas=case.replicas,
+                                   fused=case.fused)
+            v = rep.verdict()
+            decomp[name] = {
+                "t_stream_us": round(v.t_stream, 3), "t_graph_us": round(v.t_graph, 3),
+                "t_fused_us": round(v.t_fused, 3), "delta_launch_us": round(v.delta_launch, 3),
+                "delta_launch_ci": [round(c, 3) for c in v.delta_launch_ci],
+                "B_us": round(v.b_bytes_est, 3), "residual_us": round(v.residual_us, 3),
+                "bound": v.bound, "dominant": v.dominant,
+                "total_bytes": v.total_bytes, "eliminable_bytes": v.eliminable_bytes}
+            log(f"{name}: stream {v.t_stream:.2f} graph {v.t_graph:.2f} fused "
+                f"{v.t_fused:.2f} us; dL {v.delta_launch:.2f} B {v.b_bytes_est:.3f}")
+            del case, rep
+            torch.cuda.empty_cache()
+        out["decomposition"] = decomp
+
+        # ---- CPU baseline ------------------------------------------------
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        log(f"cpu baseline: {out['cpu_baseline']['value']} GB/s on "
+            f"{out['cpu_baseline']['cores']} threads")
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
