@@ -219,6 +219,10 @@ int db_tune(const char* key, int value) {
   } else if (!strcmp(key, "f4_blocks_per_cu")) {
     if (value < 1) return fail(DB_ERR_INVALID, "db_tune: f4_blocks_per_cu must be >= 1");
     t.f4_blocks_per_cu = value;
+  } else if (!strcmp(key, "f4_waves")) {
+    if (value != 0 && value != 4 && value != 8)
+      return fail(DB_ERR_INVALID, "db_tune: f4_waves must be 0, 4 or 8");
+    t.f4_waves = value;
   } else if (!strcmp(key, "f4_min_tiles")) {
     if (value < 1) return fail(DB_ERR_INVALID, "db_tune: f4_min_tiles must be >= 1");
     t.f4_min_tiles = value;

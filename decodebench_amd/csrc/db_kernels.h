@@ -10,8 +10,9 @@ namespace dbk {
 // changed at run time through db_tune() for launch-shape sweeps.
 struct Tuning {
   int gemv_waves_per_cu = 0;   // 0: choose from the row-group count
-  int f4_blocks_per_cu = 2;    // target resident F4 blocks per CU
-  int f4_min_tiles = 2;        // minimum 16-row tiles per F4 block
+  int f4_blocks_per_cu = 1;    // target F4 workgroups per CU
+  int f4_min_tiles = 2;        // minimum 16-row tiles per F4 split
+  int f4_waves = 0;            // waves per F4 workgroup (4 or 8; 0: auto)
 };
 Tuning& tuning();
 

@@ -5,27 +5,32 @@
 // query heads sharing each KV head.
 //
 // Decomposition
-//  * A workgroup (4 waves) owns one (batch, kv-head) pair and one split of the
-//    KV length; all G query heads of the pair are handled together, so every
-//    K/V byte is read from HBM exactly once.
+//  * A workgroup (NW waves) owns one (batch, kv-head) pair and one split of
+//    the KV length; all G query heads of the pair are handled together, so
+//    every K/V byte is read from HBM exactly once.  The host sizes the split
+//    count so the grid is about one workgroup per CU.
 //  * Workgroups of one pair are numbered so that they all land on the same
-//    XCD (workgroup i runs on XCD i % 8); their partial results then stay in
-//    that XCD's L2 for the combine.
-//  * A wave walks 16-row tiles.  Scores for the tile come from four
-//    v_mfma_f32_16x16x32_f16: A = the 16 x 128 K tile straight from HBM
-//    (16 B per lane per k-step), B = Q^T with the G query heads as columns
-//    (zero-padded to 16).  The accumulator lands as S[key 4g+i][head n] in
-//    lane 16g+n, register i.
+//    XCD (workgroup i is dispatched to XCD i % 8).
+//  * A wave walks 16-row tiles of its split (tile w, w + NW, ...) with two
+//    register sets of two tiles each, so two to four tiles (16-32 KB) of K
+//    and V are in flight per wave.
+//  * Scores for a tile come from four v_mfma_f32_16x16x32_f16: A = the
+//    16 x 128 K tile straight from HBM (16 B per lane per k-step), B = Q^T
+//    with the G query heads as columns (zero-padded to 16).  The accumulator
+//    lands as S[key 4g+i][head n] in lane 16g+n, register i.
 //  * Online softmax runs in base 2 (scale * log2 e folded into the scores) on
 //    the 4 keys each lane holds; the tile max crosses rows with two lane
 //    swaps.  Probabilities reach the P.V lanes through DPP row_newbcast, since
 //    lane (r, c) of the P.V layout needs keys 4r..4r+3, which live in row r.
 //  * P.V is fp32 FMA on the VALU: lane (r, c) owns d = 8c..8c+7 of every head
 //    for the V rows 4r..4r+3 of each tile.
-//  * The 4 waves merge through LDS; with S > 1 splits each workgroup writes
-//    an unnormalised partial (o, m, l) and the last workgroup of the pair to
-//    finish (a device-scope counter) merges the S partials by log-sum-exp and
-//    writes the fp16 output, then re-arms the counter for the next call.
+//  * The waves merge through LDS.  With S = 1 the workgroup writes the fp16
+//    output.  With S > 1 splits each workgroup writes an unnormalised partial
+//    (o, and the pair (m, l) per head) and a second, small launch merges the
+//    S partials of every (pair, head) by log-sum-exp.  The kernel boundary
+//    orders the partial stores before the merge loads; an in-kernel
+//    "last workgroup merges" scheme needs an L2 writeback plus a
+//    device-scope atomic per workgroup, which measured slower on MI355X.
 //
 // The merge follows the reference's two-phase split-KV form
 // (validation/src/kernels/fused/f4.cu:160-319): per-split max m, exp-sum l
@@ -37,10 +42,10 @@ namespace dbk {
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / kWave;
 constexpr int kD = 128;
 constexpr int kTile = 16;
+constexpr int kPrefetch = 4;  // tiles loaded up front on the short path
+constexpr int kMergeChunk = 8;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
 
@@ -49,8 +54,8 @@ struct F4Args {
   const _Float16* k;   // [B, Hkv, L, D]
   const _Float16* v;   // [B, Hkv, L, D]
   _Float16* o;         // [B, Hq, D]
-  unsigned* counters;  // [B * Hkv]   zero between calls
-  float* part;         // [B * Hkv, S, G * (D + 2)]
+  float2* ml;          // [B * Hkv, G, S]    (max, exp-sum) per split, base 2
+  float* opart;        // [B * Hkv, S, G, D] unnormalised outputs
   int B, Hq, Hkv, L, S;
   int ntiles;          // ceil(L / 16)
   int tps;             // tiles per split
@@ -77,18 +82,22 @@ __device__ __forceinline__ float xor_lanes(float v, int m) {
   return __shfl_xor(v, m);
 }
 
-template <int G>
-__global__ __launch_bounds__(kThreads) void f4_kernel(F4Args a) {
-  static_assert(G >= 1 && G <= 8, "query heads per KV head");
-  constexpr int kPart = G * (kD + 2);  // floats per partial record
+// exp2(m - M) with exp2(-inf - x) = 0 also when M is -inf.
+__device__ __forceinline__ float weight2(float m, float M) {
+  return m == kNegInf ? 0.0f : fast_exp2(m - M);
+}
 
-  __shared__ __align__(16) float s_o[kWaves][G][kD];  // per-wave outputs
-  __shared__ float s_m[kWaves][G];
-  __shared__ float s_l[kWaves][G];
-  __shared__ int s_last;
+template <int G, int NW>
+__global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
+  static_assert(G >= 1 && G <= 8, "query heads per KV head");
+  constexpr int kThreads = NW * kWave;
+
+  __shared__ __align__(16) float s_o[NW][G][kD];  // per-wave outputs
+  __shared__ float s_m[NW][G];
+  __shared__ float s_l[NW][G];
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
   const int n16 = lane & 15;  // MFMA column / P.V d-chunk
   const int g4 = lane >> 4;   // MFMA k-group / P.V row group
 
@@ -119,6 +128,8 @@ __global__ __launch_bounds__(kThreads) void f4_kernel(F4Args a) {
 
   const int t_begin = split * a.tps;
   const int t_end = min(a.ntiles, t_begin + a.tps);
+  const int first = t_begin + wave;
+  const int nt = first < t_end ? (t_end - first + NW - 1) / NW : 0;
   const int last_row = a.L - 1;
 
   float o[G][8];
@@ -192,26 +203,56 @@ __global__ __launch_bounds__(kThreads) void f4_kernel(F4Args a) {
     }
   };
 
-  // ---- stream this wave's tiles: wave w takes t_begin + w, + 4, ... -----
-  {
-    u4 kb[2][4], vb[2][4];
-    int tile = t_begin + wave;
-    if (tile < t_end) load_tile(kb[0], vb[0], tile);
-    for (;;) {
-      if (tile >= t_end) break;
-      int nxt = tile + kWaves;
-      if (nxt < t_end) load_tile(kb[1], vb[1], nxt);
-      compute_tile(kb[0], vb[0], tile);
-      tile = nxt;
-      if (tile >= t_end) break;
-      nxt = tile + kWaves;
-      if (nxt < t_end) load_tile(kb[0], vb[0], nxt);
-      compute_tile(kb[1], vb[1], tile);
-      tile = nxt;
+  // ---- stream this wave's tiles ------------------------------------------
+  // Long runs use two register sets of two tiles each.  An iteration loads
+  // set B, consumes set A, reloads A and consumes B, so four tiles are in
+  // flight between consumptions and every wait is for one set only.  (Set B
+  // is loaded and consumed in the same iteration, which keeps the compiler
+  // from draining all loads at the loop header, as it does for a ring whose
+  // slots are consumed before they are reloaded.)
+  if (nt >= 6) {
+    u4 ka[2][4], va[2][4], kb[2][4], vb[2][4];
+    load_tile(ka[0], va[0], first);
+    load_tile(ka[1], va[1], first + NW);
+    int k = 0;
+    for (; k + 6 <= nt; k += 4) {
+      load_tile(kb[0], vb[0], first + NW * (k + 2));
+      load_tile(kb[1], vb[1], first + NW * (k + 3));
+      compute_tile(ka[0], va[0], first + NW * k);
+      compute_tile(ka[1], va[1], first + NW * (k + 1));
+      load_tile(ka[0], va[0], first + NW * (k + 4));
+      load_tile(ka[1], va[1], first + NW * (k + 5));
+      compute_tile(kb[0], vb[0], first + NW * (k + 2));
+      compute_tile(kb[1], vb[1], first + NW * (k + 3));
     }
+    // 2 <= nt - k <= 5 tiles remain; set A holds tiles k and k + 1.
+    if (k + 2 < nt) load_tile(kb[0], vb[0], first + NW * (k + 2));
+    if (k + 3 < nt) load_tile(kb[1], vb[1], first + NW * (k + 3));
+    compute_tile(ka[0], va[0], first + NW * k);
+    compute_tile(ka[1], va[1], first + NW * (k + 1));
+    if (k + 4 < nt) load_tile(ka[0], va[0], first + NW * (k + 4));
+    if (k + 2 < nt) compute_tile(kb[0], vb[0], first + NW * (k + 2));
+    if (k + 3 < nt) compute_tile(kb[1], vb[1], first + NW * (k + 3));
+    if (k + 4 < nt) compute_tile(ka[0], va[0], first + NW * (k + 4));
+  } else {
+    // Fewer than 2 * kPrefetch tiles: load what fits, refill once.
+    u4 kb[kPrefetch][4], vb[kPrefetch][4];
+#pragma unroll
+    for (int s = 0; s < kPrefetch; ++s)
+      if (s < nt) load_tile(kb[s], vb[s], first + NW * s);
+#pragma unroll
+    for (int s = 0; s < kPrefetch; ++s) {
+      if (s < nt) {
+        compute_tile(kb[s], vb[s], first + NW * s);
+        if (s + kPrefetch < nt) load_tile(kb[s], vb[s], first + NW * (s + kPrefetch));
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < kPrefetch; ++s)
+      if (kPrefetch + s < nt) compute_tile(kb[s], vb[s], first + NW * (kPrefetch + s));
   }
 
-  // ---- merge the 4 waves of the workgroup through LDS -------------------
+  // ---- merge the waves of the workgroup through LDS ---------------------
   float l_tot = l_run + xor_lanes(l_run, 16);
   l_tot += xor_lanes(l_tot, 32);
   if (lane < G) {
@@ -236,121 +277,137 @@ __global__ __launch_bounds__(kThreads) void f4_kernel(F4Args a) {
   }
   __syncthreads();
 
-  const size_t rec = ((size_t)pair * a.S + split) * kPart;
   for (int idx = threadIdx.x; idx < G * kD; idx += kThreads) {
     const int h = idx / kD, d = idx % kD;
     float M = kNegInf;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][h]);
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][h]);
     float ow = 0.0f, lw = 0.0f;
-    if (M != kNegInf) {
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const float e = fast_exp2(s_m[w][h] - M);
-        ow += e * s_o[w][h][d];
-        lw += e * s_l[w][h];
-      }
+    for (int w = 0; w < NW; ++w) {
+      const float e = weight2(s_m[w][h], M);
+      ow += e * s_o[w][h][d];
+      lw += e * s_l[w][h];
     }
     if (a.S == 1) {
       a.o[q_base + (size_t)h * kD + d] = to_h(ow / lw);
     } else {
-      a.part[rec + idx] = ow;
-      if (d == 0) {
-        a.part[rec + G * kD + h] = M;
-        a.part[rec + G * kD + G + h] = lw;
-      }
+      a.opart[(((size_t)pair * a.S + split) * G + h) * kD + d] = ow;
+      if (d == 0) a.ml[((size_t)pair * G + h) * a.S + split] = make_float2(M, lw);
     }
   }
   if (a.S == 1) return;
 
-  // ---- split combine: the last workgroup of the pair merges S partials ---
-  __threadfence();  // publish this thread's partial stores device-wide
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(
-        &a.counters[pair], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (prev == (unsigned)(a.S - 1));
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();  // acquire side: see every other workgroup's partials
+}
 
-  // Reuse s_o as scratch: weights w[s][h] = e^{m_s - M_h} / L_h.
-  float* s_w = &s_o[0][0][0];
-  constexpr int kScratch = kWaves * G * kD;
-  const float* base = a.part + (size_t)pair * a.S * kPart;
-  const int sg = a.S * G;  // <= kScratch / 2 (checked on the host)
-  for (int i = threadIdx.x; i < sg; i += kThreads) {
-    const int s = i / G, h = i % G;
-    s_w[i] = base[(size_t)s * kPart + G * kD + h];              // m
-    s_w[sg + i] = base[(size_t)s * kPart + G * kD + G + h];     // l
-  }
-  __syncthreads();
-  if (threadIdx.x < G) {
-    const int h = threadIdx.x;
-    float M = kNegInf;
-    for (int s = 0; s < a.S; ++s) M = fmaxf(M, s_w[s * G + h]);
-    float Lsum = 0.0f;
-    for (int s = 0; s < a.S; ++s) {
-      const float ms = s_w[s * G + h];
-      if (ms != kNegInf) Lsum += fast_exp2(ms - M) * s_w[sg + s * G + h];
-    }
-    s_m[0][h] = M;
-    s_l[0][h] = 1.0f / Lsum;
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < sg; i += kThreads) {
-    const int h = i % G;
-    const float ms = s_w[i];
-    s_w[i] = (ms == kNegInf) ? 0.0f : fast_exp2(ms - s_m[0][h]) * s_l[0][h];
-  }
-  __syncthreads();
-  static_assert(kScratch >= 2, "scratch");
-  for (int idx = threadIdx.x; idx < G * kD; idx += kThreads) {
-    const int h = idx / kD;
-    float acc = 0.0f;
-    int s = 0;
-    for (; s + 8 <= a.S; s += 8) {
-      float vals[8];
+// Second launch of a split call: one workgroup per (pair, query head).
+// Thread (grp, d4) merges the splits grp, grp + 8, ... of float4 slot d4 by
+// online log-sum-exp in base 2 (all loads of a chunk of 8 splits are issued
+// together), then the 8 groups merge through LDS and write the fp16 output.
+// The kernel boundary orders the partial stores of the first launch before
+// these loads.
+__global__ __launch_bounds__(256) void f4_combine(F4Args a, int G) {
+  constexpr int kGroups = 8;
+  __shared__ float s_c[kGroups][kD / 4][6];
+  const int pair = blockIdx.x / G, h = blockIdx.x % G;
+  const int d4 = threadIdx.x & (kD / 4 - 1), grp = threadIdx.x / (kD / 4);
+  const f4* opart4 = reinterpret_cast<const f4*>(a.opart);
+  const float2* mlp = a.ml + ((size_t)pair * G + h) * a.S;
+  float M = kNegInf, Ls = 0.0f;
+  f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = grp; s0 < a.S; s0 += kGroups * kMergeChunk) {
+    f4 ov[kMergeChunk];
+    float2 mv[kMergeChunk];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) vals[u] = base[(size_t)(s + u) * kPart + idx];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) acc = fmaf(s_w[(s + u) * G + h], vals[u], acc);
+    for (int j = 0; j < kMergeChunk; ++j) {
+      const int s = s0 + kGroups * j;
+      if (s < a.S) {
+        ov[j] = opart4[(((size_t)pair * a.S + s) * G + h) * (kD / 4) + d4];
+        mv[j] = mlp[s];
+      } else {
+        ov[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        mv[j] = make_float2(kNegInf, 0.0f);
+      }
     }
-    for (; s < a.S; ++s) acc = fmaf(s_w[s * G + h], base[(size_t)s * kPart + idx], acc);
-    a.o[q_base + idx] = to_h(acc);
+    float Mn = M;
+#pragma unroll
+    for (int j = 0; j < kMergeChunk; ++j) Mn = fmaxf(Mn, mv[j].x);
+    const float r = weight2(M, Mn);
+    Ls *= r;
+    acc *= r;
+#pragma unroll
+    for (int j = 0; j < kMergeChunk; ++j) {
+      const float w = weight2(mv[j].x, Mn);
+      Ls = fmaf(w, mv[j].y, Ls);
+      acc += w * ov[j];
+    }
+    M = Mn;
   }
-  if (threadIdx.x == 0)
-    __hip_atomic_store(&a.counters[pair], 0u, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+  float* c = s_c[grp][d4];
+  c[0] = M;
+  c[1] = Ls;
+  c[2] = acc[0];
+  c[3] = acc[1];
+  c[4] = acc[2];
+  c[5] = acc[3];
+  __syncthreads();
+  if (grp != 0) return;
+  float Mt = kNegInf;
+#pragma unroll
+  for (int gi = 0; gi < kGroups; ++gi) Mt = fmaxf(Mt, s_c[gi][d4][0]);
+  float Lt = 0.0f;
+  f4 at = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int gi = 0; gi < kGroups; ++gi) {
+    const float* cc = s_c[gi][d4];
+    const float w = weight2(cc[0], Mt);
+    Lt = fmaf(w, cc[1], Lt);
+    at += w * f4{cc[2], cc[3], cc[4], cc[5]};
+  }
+  const float inv = 1.0f / Lt;
+  const int b = pair / a.Hkv, kvh = pair % a.Hkv;
+  const size_t o_base = ((size_t)b * a.Hq + (size_t)kvh * G + h) * kD;
+  uint2 packed;
+  packed.x = pack_h2(at[0] * inv, at[1] * inv);
+  packed.y = pack_h2(at[2] * inv, at[3] * inv);
+  *reinterpret_cast<uint2*>(a.o + o_base + (size_t)d4 * 4) = packed;
 }
 
 using F4Fn = void (*)(F4Args);
 
-F4Fn pick_f4(int G) {
+// Eight-wave workgroups exist for G <= 4 only: with G = 8 the per-lane
+// output accumulators do not fit the 256 registers a 512-thread workgroup
+// leaves each wave.
+F4Fn pick_kernel(int G, int waves) {
+  if (waves == 8) {
+    switch (G) {
+      case 1: return f4_kernel<1, 8>;
+      case 2: return f4_kernel<2, 8>;
+      default: return f4_kernel<4, 8>;
+    }
+  }
   switch (G) {
-    case 1: return f4_kernel<1>;
-    case 2: return f4_kernel<2>;
-    case 4: return f4_kernel<4>;
-    default: return f4_kernel<8>;
+    case 1: return f4_kernel<1, 4>;
+    case 2: return f4_kernel<2, 4>;
+    case 4: return f4_kernel<4, 4>;
+    default: return f4_kernel<8, 4>;
   }
 }
 
-constexpr size_t kCounterBytes(int pairs) {
-  return (((size_t)pairs * sizeof(unsigned)) + 255) / 256 * 256;
-}
+size_t round256(size_t n) { return (n + 255) / 256 * 256; }
 
 }  // namespace
 
-// Largest split count the in-kernel combine supports for group size G: the
-// S x G (m, l) pairs must fit in the workgroup's LDS scratch.
-int f4_max_splits(int G) { return (kWaves * G * kD) / (2 * G); }
+// Largest split count of one launch.
+int f4_max_splits(int G) {
+  (void)G;
+  return 256;
+}
 
 size_t f4_workspace_bytes(int B, int Hq, int Hkv, int S, int D) {
   const int G = Hq / Hkv;
-  const int pairs = B * Hkv;
-  return kCounterBytes(pairs) +
-         (size_t)pairs * S * G * (D + 2) * sizeof(float);
+  const size_t pairs = (size_t)B * Hkv;
+  return round256(pairs * G * S * sizeof(float2)) + pairs * S * G * D * sizeof(float);
 }
 
 int f4_choose_splits(int B, int Hkv, int L, int cu_count) {
@@ -368,7 +425,6 @@ int f4_choose_splits(int B, int Hkv, int L, int cu_count) {
 hipError_t launch_f4(const void* q, const void* k, const void* v, void* o,
                      void* ws, int B, int Hq, int Hkv, int L, int D, int S,
                      float scale, hipStream_t stream) {
-  (void)D;
   const int G = Hq / Hkv;
   const int pairs = B * Hkv;
   F4Args a;
@@ -376,10 +432,6 @@ hipError_t launch_f4(const void* q, const void* k, const void* v, void* o,
   a.k = static_cast<const _Float16*>(k);
   a.v = static_cast<const _Float16*>(v);
   a.o = static_cast<_Float16*>(o);
-  a.counters = static_cast<unsigned*>(ws);
-  a.part = ws ? reinterpret_cast<float*>(static_cast<char*>(ws) +
-                                         kCounterBytes(pairs))
-              : nullptr;
   a.B = B;
   a.Hq = Hq;
   a.Hkv = Hkv;
@@ -389,9 +441,24 @@ hipError_t launch_f4(const void* q, const void* k, const void* v, void* o,
   a.S = min(S, a.ntiles);
   a.tps = (a.ntiles + a.S - 1) / a.S;
   a.S = (a.ntiles + a.tps - 1) / a.tps;
+  // The partial areas are laid out for the caller's S (the size it
+  // allocated); the kernels use the first a.S <= S records of each pair.
+  char* base = static_cast<char*>(ws);
+  a.ml = reinterpret_cast<float2*>(base);
+  a.opart = base ? reinterpret_cast<float*>(base + round256((size_t)pairs * G * S * sizeof(float2)))
+                 : nullptr;
   a.xcd_map = (pairs % 8 == 0) ? 1 : 0;
   a.scale_log2 = scale * kLog2e;
-  hipLaunchKernelGGL(pick_f4(G), dim3(pairs * a.S), dim3(kThreads), 0, stream, a);
+  (void)D;
+  int waves = tuning().f4_waves > 0 ? tuning().f4_waves : (a.tps >= 16 ? 8 : 4);
+  if (G == 8) waves = 4;
+  hipLaunchKernelGGL(pick_kernel(G, waves), dim3(pairs * a.S), dim3(waves * kWave), 0,
+                     stream, a);
+  if (a.S > 1) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(f4_combine, dim3(pairs * G), dim3(256), 0, stream, a, G);
+  }
   return hipGetLastError();
 }
 

@@ -60,7 +60,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   __shared__ float red[kWaves][NB];
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
   const int b0 = blockIdx.y * NB;
   const int nb = min(NB, a.B - b0);
   const int stride_waves = gridDim.x * kWaves;
@@ -85,34 +85,74 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     }
   };
 
+  // ---- activation chunks (and gamma) of the first kPre passes -> registers.
+  // They are loaded before the first weight tile, so they arrive first and
+  // the activation prologue overlaps the weight stream instead of waiting
+  // behind it (loads complete in issue order).  The loads are unconditional
+  // (clamped addresses, masked afterwards) and their uses straight-line, so
+  // the compiler waits for them alone and not for the weights.
+  constexpr int kPre = 2;  // covers K <= 2 * 256 * 8 = 4096 with no reload
+  u4 xr[kPre][NB];
+  u4 gr[kPre];
+#pragma unroll
+  for (int i = 0; i < kPre; ++i) {
+    const int c = min((int)threadIdx.x + i * kThreads, a.kchunks - 1);
+    gr[i] = u4{0, 0, 0, 0};
+    if constexpr (MODE == kGemvRmsNorm) gr[i] = ld16(a.gamma + (size_t)c * 8);
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+      xr[i][b] = ld16(a.x + (size_t)(b0 + min(b, nb - 1)) * a.K + (size_t)c * 8);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // The first tile load is unconditional (a wave past the last group loads
+  // the last group's tile and never uses it), so no branch merges a state
+  // with and without the weight loads in flight.
   u4 wbuf[2][NW][R][U];
   int grp = blockIdx.x * kWaves + wave;
   int st = 0;
-  if (grp < a.groups) load_tile(wbuf[0], grp, 0);
+  load_tile(wbuf[0], min(grp, a.groups - 1), 0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  const u4 zero4 = {0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < kPre; ++i) {
+    const bool valid_c = (int)threadIdx.x + i * kThreads < a.kchunks;
+    gr[i] = valid_c ? gr[i] : zero4;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) xr[i][b] = (valid_c && b < nb) ? xr[i][b] : zero4;
+  }
+  // Passes beyond kPre (K > 4096) read x and gamma again.
+  const int c_rest = threadIdx.x + kPre * kThreads;
+  auto x_rest = [&](int c, int b) -> u4 {
+    return (c < a.kchunks && b < nb) ? ld16(a.x + (size_t)(b0 + b) * a.K + (size_t)c * 8)
+                                     : zero4;
+  };
 
   // ---- activation rows -> LDS (once per workgroup) ----------------------
   if constexpr (MODE == kGemvRmsNorm) {
     float ss[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) ss[b] = 0.0f;
-    for (int c = threadIdx.x; c < a.kchunks; c += kThreads) {
+    auto add_sq = [&](const u4& v, float& acc) {
 #pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        if (b < nb) {
-          const u4 v = ld16(a.x + (size_t)(b0 + b) * a.K + (size_t)c * 8);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const h2 p = as_h2(v[i]);
-            const float lo = (float)p[0], hi = (float)p[1];
-            ss[b] += lo * lo + hi * hi;
-          }
-        }
+      for (int j = 0; j < 4; ++j) {
+        const h2 p = as_h2(v[j]);
+        const float lo = (float)p[0], hi = (float)p[1];
+        acc += lo * lo + hi * hi;
       }
-    }
+    };
+#pragma unroll
+    for (int i = 0; i < kPre; ++i)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) add_sq(xr[i][b], ss[b]);
+    for (int c = c_rest; c < a.kchunks; c += kThreads)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) add_sq(x_rest(c, b), ss[b]);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      const float s = wave_sum(ss[b]);
-      if (lane == 0) red[wave][b] = s;
+      const float sum = wave_sum(ss[b]);
+      if (lane == 0) red[wave][b] = sum;
     }
     __syncthreads();
     float inv[NB];
@@ -121,38 +161,43 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
       const float tot = (red[0][b] + red[1][b]) + (red[2][b] + red[3][b]);
       inv[b] = 1.0f / sqrtf(tot / (float)a.K + a.eps);
     }
-    for (int c = threadIdx.x; c < a.kp8; c += kThreads) {
-      const bool valid_c = c < a.kchunks;
-      const u4 gv = valid_c ? ld16(a.gamma + (size_t)c * 8) : u4{0, 0, 0, 0};
+    // fp16(x * inv_rms), then fp16(that * gamma): the fp16 x fp16 product is
+    // exact in fp32, so one rounding matches torch.  Zero chunks stay zero.
+    auto norm = [&](const u4& xv, const u4& gv, float iv) -> u4 {
+      u4 out;
 #pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        u4 out = {0, 0, 0, 0};
-        if (valid_c && b < nb) {
-          const u4 xv = ld16(a.x + (size_t)(b0 + b) * a.K + (size_t)c * 8);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const h2 xp = as_h2(xv[i]);
-            const h2 gp = as_h2(gv[i]);
-            // fp16(x * inv_rms), then fp16(that * gamma): the fp16 x fp16
-            // product is exact in fp32, so one rounding matches torch.
-            const float n0 = (float)to_h((float)xp[0] * inv[b]);
-            const float n1 = (float)to_h((float)xp[1] * inv[b]);
-            out[i] = pack_h2(n0 * (float)gp[0], n1 * (float)gp[1]);
-          }
-        }
-        xs[b * a.kp8 + c] = out;
+      for (int j = 0; j < 4; ++j) {
+        const h2 xp = as_h2(xv[j]);
+        const h2 gp = as_h2(gv[j]);
+        const float n0 = (float)to_h((float)xp[0] * iv);
+        const float n1 = (float)to_h((float)xp[1] * iv);
+        out[j] = pack_h2(n0 * (float)gp[0], n1 * (float)gp[1]);
       }
+      return out;
+    };
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) {
+      const int c = threadIdx.x + i * kThreads;
+      if (c < a.kp8)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) xs[b * a.kp8 + c] = norm(xr[i][b], gr[i], inv[b]);
+    }
+    for (int c = c_rest; c < a.kp8; c += kThreads) {
+      const u4 gv = c < a.kchunks ? ld16(a.gamma + (size_t)c * 8) : zero4;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) xs[b * a.kp8 + c] = norm(x_rest(c, b), gv, inv[b]);
     }
   } else {
-    for (int c = threadIdx.x; c < a.kp8; c += kThreads) {
 #pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        u4 out = {0, 0, 0, 0};
-        if (c < a.kchunks && b < nb)
-          out = ld16(a.x + (size_t)(b0 + b) * a.K + (size_t)c * 8);
-        xs[b * a.kp8 + c] = out;
-      }
+    for (int i = 0; i < kPre; ++i) {
+      const int c = threadIdx.x + i * kThreads;
+      if (c < a.kp8)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) xs[b * a.kp8 + c] = xr[i][b];
     }
+    for (int c = c_rest; c < a.kp8; c += kThreads)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) xs[b * a.kp8 + c] = x_rest(c, b);
   }
   __syncthreads();
 

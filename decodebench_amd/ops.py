@@ -222,11 +222,11 @@ def f4_default_splits(B: int, Hkv: int, L: int, device=None) -> int:
 
 
 def f4_workspace(B: int, Hq: int, Hkv: int, L: int, D: int, S: int, device):
-    """Zero-filled workspace for db_f4_splitkv, cached per shape and device.
+    """Workspace for db_f4_splitkv, cached per size and device.
 
-    The kernel re-arms the workspace after every call, so one cached buffer
-    serves every later call with the same shape on that device (calls on that
-    buffer must not overlap in time)."""
+    The library needs no initialisation of it and keeps nothing in it between
+    calls, so one buffer serves every later call of that size on that device
+    (calls sharing it must not overlap in time)."""
     import torch
 
     nbytes = int(load_library().db_f4_workspace_bytes(B, Hq, Hkv, L, D, S))
@@ -236,7 +236,7 @@ def f4_workspace(B: int, Hq: int, Hkv: int, L: int, D: int, S: int, device):
     key = (dev.index if dev.index is not None else torch.cuda.current_device(), nbytes)
     ws = _ws_cache.get(key)
     if ws is None:
-        ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
         _ws_cache[key] = ws
     return ws
 

@@ -90,22 +90,23 @@ int db_gemv(const void* x, const void* W, const float* w_scale, void* y,
             int B, int K, int N, int w_dtype, void* stream);
 
 /* Split count the library picks for F4 when the caller has no preference:
- * enough (batch, kv-head, split) workgroups to fill `cu_count` CUs while every
- * split keeps at least two 16-row tiles.  Replaces the fixed L/128 default and
+ * about one (batch, kv-head, split) workgroup per CU of `cu_count` while
+ * every split keeps at least four 16-row tiles.  Replaces the fixed L/128 default and
  * DECODEBENCH_F4_SPLITS override of the reference harness
  * (validation/src/bench/bench_variant.cu:714-719). */
 int db_f4_default_splits(int B, int Hkv, int L, int cu_count);
 
 /* Bytes of caller-owned workspace db_f4_splitkv needs for S splits (0 when
- * S == 1).  The workspace must be zero-filled before its first use; the
- * kernel leaves it re-armed (its counters back at zero) after every call. */
+ * S == 1): the per-split partial records.  Its contents need no
+ * initialisation and are not needed after the call. */
 size_t db_f4_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S);
 
 /* F4: o[b,h,:] = softmax(scale * q[b,h,:] . K[b,h/G,:,:]^T) . V[b,h/G,:,:]
  * for G = Hq / Hkv query heads per KV head (grouped-query attention), fp32
  * softmax and accumulation, fp16 output.  The KV length is cut into S splits
- * whose partial (max, exp-sum, unnormalised output) records are merged by
- * log-sum-exp inside the same launch.
+ * whose partial (max, exp-sum, unnormalised output) records go to the
+ * workspace; a second launch on the same stream merges them by log-sum-exp
+ * (one launch in total when S == 1).
  * Replaces f4_partial_kernel + f4_reduce_kernel
  * (validation/src/kernels/fused/f4.cu:173-319) and the reference stages
  * scores, softmax, weighted_v (src/decodebench/demos/llama_decode.py:120-134).
@@ -117,8 +118,9 @@ int db_f4_splitkv(const void* q, const void* k, const void* v, void* o,
                   int D, int S, float scale, void* stream);
 
 /* Launch-geometry knobs for tuning sweeps ("gemv_waves_per_cu",
- * "f4_blocks_per_cu", "f4_min_tiles"); value <= 0 restores the default for
- * the GEMV knob.  No counterpart in the reference. */
+ * "f4_blocks_per_cu", "f4_min_tiles", "f4_waves"); value <= 0 restores the
+ * default for the GEMV knob, 0 for "f4_waves" (4 or 8 waves per workgroup).
+ * No counterpart in the reference. */
 int db_tune(const char* key, int value);
 
 #ifdef __cplusplus

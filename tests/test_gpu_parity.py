@@ -172,22 +172,23 @@ def test_f4_full_batch_split_invariance(L):
     assert rel_l2(outs[-1][7:], exact7) < F4_REL_L2
 
 
-def test_f4_workspace_rearms_between_calls():
-    """The in-kernel split counter must be back at zero after every call:
-    repeated calls (and a different split count on the same workspace) give
-    bitwise-identical results."""
+def test_f4_workspace_reuse_is_deterministic():
+    """One workspace serves any number of calls: repeated calls (and a
+    different split count on the same workspace, whose stale records must not
+    leak into the result) give bitwise-identical results; a workspace full of
+    garbage (NaN bytes) before the first call changes nothing."""
     q, K, V = f4_inputs(1, 32, 8, 8192, 5)
     qd, Kd, Vd = q.cuda(), K.cuda(), V.cuda()
-    ws = torch.zeros(ops.load_library().db_f4_workspace_bytes(1, 32, 8, 8192, 128, 64),
-                     dtype=torch.uint8, device="cuda")
+    nbytes = ops.load_library().db_f4_workspace_bytes(1, 32, 8, 8192, 128, 64)
+    ws = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device="cuda")
     first = ops.f4_flashdecode(qd, Kd, Vd, n_splits=64, workspace=ws)
     for _ in range(20):
         again = ops.f4_flashdecode(qd, Kd, Vd, n_splits=64, workspace=ws)
         assert torch.equal(first, again)
     other = ops.f4_flashdecode(qd, Kd, Vd, n_splits=16, workspace=ws)
     assert rel_l2(other.float().cpu().numpy(), first.float().cpu().numpy()) < 2e-3
-    counters = ws[: 8 * 4].view(torch.int32)
-    assert int(counters.abs().sum().item()) == 0
+    exact = cref.attention(q.numpy(), K.numpy(), V.numpy())
+    assert rel_l2(first.float().cpu().numpy(), exact) < F4_REL_L2
 
 
 def test_f4_gqa_equals_mha_on_gpu():
