@@ -58,6 +58,11 @@ def parse_args(argv=None):
                     help="bound on the CPU baseline sample")
     ap.add_argument("--trials", type=int, default=12,
                     help="trials per variant in the decomposition")
+    ap.add_argument("--profile-pass", metavar="MANIFEST",
+                    help="run the workload for rocprofv3 instead: calibration copies, then "
+                         "every kernel eagerly; write the launch manifest to MANIFEST and exit")
+    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.json"),
+                    help="rocprofv3 traffic summary (decodebench_amd.rocprof) for roofline.traffic")
     return ap.parse_args(argv)
 
 
@@ -142,9 +147,66 @@ def kernel_row(case, us: float) -> dict:
             "replicas": len(case.replicas), "shape": case.shape}
 
 
+# ------------------------------------------------------------ profile pass
+PROFILE_WORKLOADS = (("f1_cfg1", dict(name="f1")), ("f1_qkv_cfg3", dict(name="f1_qkv")),
+                     ("f2_cfg2", dict(name="f2")), ("f4_L1024", dict(name="f4", L=1024)),
+                     ("f4_L8192", dict(name="f4", L=8192)), ("f4_L32768", dict(name="f4", L=32768)))
+
+
+def profile_pass(manifest_path: str, calls: int = 24, warmup: int = 4) -> int:
+    """Launch sequence for decodebench_amd.rocprof: calibration copies first,
+    then each workload's fused kernels eagerly over cache-defeating replicas."""
+    import torch
+
+    from decodebench_amd import ops
+    from decodebench_amd.demos.llama_decode import build_config
+
+    ops.load_library()
+    copy_bytes, copy_calls = 512 << 20, 3
+    src = torch.empty(copy_bytes, dtype=torch.uint8, device="cuda")
+    src.fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(copy_calls):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    workloads = []
+    for label, kw in PROFILE_WORKLOADS:
+        case = build_config(batch=1, **kw)
+        per_call = 1
+        if kw["name"] == "f4":
+            s = case.shape["S"] or ops.f4_default_splits(1, case.shape["Hkv"], case.shape["L"])
+            per_call = 2 if s > 1 else 1
+        n = len(case.replicas)
+        for i in range(calls):
+            case.fused(case.replicas[i % n])
+        torch.cuda.synchronize()
+        workloads.append({"label": label, "calls": calls, "warmup": warmup,
+                          "kernels_per_call": per_call,
+                          "algorithmic_bytes": case.algorithmic_bytes})
+        log(f"profile pass: {label} x {calls}")
+        del case
+        torch.cuda.empty_cache()
+    with open(manifest_path, "w") as f:
+        json.dump({"copy_bytes": copy_bytes, "copy_calls": copy_calls,
+                   "workloads": workloads}, f, indent=1)
+    return 0
+
+
+def load_traffic(path: str) -> dict:
+    try:
+        with open(path) as f:
+            return json.load(f).get("workloads", {})
+    except (OSError, ValueError):
+        return {}
+
+
 # ------------------------------------------------------------ CPU baseline
-def cpu_baseline(seconds: float) -> dict:
-    """F2 (config 2, B = 1) through the torch CPU stages, time-bounded."""
+def cpu_baseline(seconds: float, replicas: int = 3) -> dict:
+    """F2 (config 2, B = 1) through the torch CPU stages, time-bounded.
+
+    Calls rotate over ``replicas`` weight copies (705 MB at 3) so the sample
+    is not served from a large host L3."""
     import torch
 
     from oracle import stages
@@ -154,13 +216,15 @@ def cpu_baseline(seconds: float) -> dict:
     x = torch.randn(1, K, generator=gen).half()
     Wg = (torch.randn(N, K, generator=gen) * 0.02).half()
     Wu = (torch.randn(N, K, generator=gen) * 0.02).half()
+    reps = [(Wg, Wu)] + [(Wg.clone(), Wu.clone()) for _ in range(replicas - 1)]
     nbytes = 2 * N * K * 2 + (K + N) * 2
     stages.f2(x, Wg, Wu)  # warm-up
     times = []
     t_end = time.perf_counter() + seconds
     while time.perf_counter() < t_end or len(times) < 3:
+        wg, wu = reps[len(times) % replicas]
         t0 = time.perf_counter()
-        stages.f2(x, Wg, Wu)
+        stages.f2(x, wg, wu)
         times.append(time.perf_counter() - t0)
     times.sort()
     med = times[len(times) // 2]
@@ -176,8 +240,8 @@ def cpu_baseline(seconds: float) -> dict:
     return {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s",
             "cores": torch.get_num_threads(), "kind": "port",
             "sample": (f"F2 B=1 Wg/Wu[14336,4096] fp16 via oracle/stages.py (torch CPU), "
-                       f"{len(times)} calls in ~{seconds:.0f} s, median "
-                       f"{med * 1e6:.0f} us/call"),
+                       f"{len(times)} calls over {replicas} weight replicas in "
+                       f"~{seconds:.0f} s, median {med * 1e6:.0f} us/call"),
             "us_per_call": round(med * 1e6, 1), "cpu_model": cpu_model,
             "os_cpu_count": os.cpu_count()}
 
@@ -200,12 +264,16 @@ def main(argv=None) -> int:
     from decodebench_amd import ops
     from decodebench_amd.demos.llama_decode import build_config
 
+    if args.profile_pass:
+        return profile_pass(args.profile_pass)
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
     ops.load_library()
     dev_name = torch.cuda.get_device_name(0)
     log(f"device {dev_name}, {ops.cu_count()} CUs")
+
+    traffic = load_traffic(args.traffic)
 
     # ---- headline: F2, config 2, batch 1 --------------------------------
     head = build_config("f2", batch=1)
@@ -228,7 +296,10 @@ def main(argv=None) -> int:
                    "weight_replicas": len(head.replicas), "device": dev_name},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "gemv_kernel<2,...> (F2 SwiGLU mode)",
+                     "traffic": traffic.get("f2_cfg2", {}).get("traffic_bytes"),
+                     "traffic_source": (os.path.relpath(args.traffic, ROOT)
+                                        if "f2_cfg2" in traffic else None),
+                     "kernel": "gemv_kernel<2,...> (F2 SwiGLU mode)",
                      "algorithmic_bytes_per_launch": head.algorithmic_bytes,
                      "avg_launch_us": round(us, 3)},
     }
@@ -248,6 +319,7 @@ def main(argv=None) -> int:
             us_k, launches = time_graph_launches(case)
             kernels[name] = kernel_row(case, us_k)
             kernels[name]["launches_per_graph"] = launches
+            kernels[name]["traffic_bytes"] = traffic.get(name, {}).get("traffic_bytes")
             log(f"{name}: {us_k:.2f} us, {kernels[name]['GB/s']:.0f} GB/s")
             del case
             torch.cuda.empty_cache()

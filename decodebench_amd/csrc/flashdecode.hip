@@ -309,7 +309,10 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
 __global__ __launch_bounds__(256) void f4_combine(F4Args a, int G) {
   constexpr int kGroups = 8;
   __shared__ float s_c[kGroups][kD / 4][6];
-  const int pair = blockIdx.x / G, h = blockIdx.x % G;
+  // blockIdx = h * pairs + pair: with the XCD-aware numbering of the first
+  // launch, the merge of a pair runs on the XCD whose L2 holds its partials.
+  const int pairs = a.B * a.Hkv;
+  const int pair = blockIdx.x % pairs, h = blockIdx.x / pairs;
   const int d4 = threadIdx.x & (kD / 4 - 1), grp = threadIdx.x / (kD / 4);
   const f4* opart4 = reinterpret_cast<const f4*>(a.opart);
   const float2* mlp = a.ml + ((size_t)pair * G + h) * a.S;

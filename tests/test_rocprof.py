@@ -1,0 +1,102 @@
+"""The rocprofv3 summary pipeline (decodebench_amd.rocprof) on synthetic CSVs.
+
+Mirrors what the reference tests for its NCU parser (round detection and
+per-kernel reduction, validation/analysis/parse_ncu.py:26-148): dispatches are
+assigned to workloads in launch order, warm-up calls are dropped, counters are
+scaled by the calibration copy, and a profile that does not match its manifest
+fails loudly instead of producing numbers.
+"""
+
+import csv
+
+import pytest
+
+from decodebench_amd import rocprof
+
+MANIFEST = {
+    "copy_bytes": 1 << 20, "copy_calls": 2,
+    "workloads": [
+        {"label": "gemv", "calls": 3, "warmup": 1, "kernels_per_call": 1,
+         "algorithmic_bytes": 1000},
+        {"label": "attn", "calls": 2, "warmup": 0, "kernels_per_call": 2,
+         "algorithmic_bytes": 5000},
+    ],
+}
+
+# (name, duration ns, FETCH KiB, WRITE KiB) in dispatch order; a foreign
+# kernel sits between workloads and must be ignored.
+ROWS = [
+    ("__amd_rocclr_copyBuffer", 900, 512.0, 1024.0),
+    ("__amd_rocclr_copyBuffer", 900, 512.0, 1024.0),
+    ("void at::native::fill", 10, 0.0, 4.0),
+    ("void dbk::(anonymous namespace)::gemv_kernel<1>(args)", 9000, 50.0, 1.0),  # warm-up
+    ("void dbk::(anonymous namespace)::gemv_kernel<1>(args)", 2000, 0.5, 0.25),
+    ("void dbk::(anonymous namespace)::gemv_kernel<1>(args)", 4000, 0.5, 0.25),
+    ("void at::native::copy", 10, 1.0, 1.0),
+    ("void dbk::(anonymous namespace)::f4_kernel<4, 8>(args)", 3000, 2.0, 0.5),
+    ("void dbk::(anonymous namespace)::f4_combine(args, int)", 1000, 0.5, 0.0625),
+    ("void dbk::(anonymous namespace)::f4_kernel<4, 8>(args)", 5000, 2.0, 0.5),
+    ("void dbk::(anonymous namespace)::f4_combine(args, int)", 1000, 0.5, 0.0625),
+]
+
+
+def write_trace(path):
+    with open(path, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Kind", "Dispatch_Id", "Kernel_Name", "Grid_Size_X", "Workgroup_Size_X",
+                    "Start_Timestamp", "End_Timestamp"])
+        t = 1000
+        for i, (name, dur, _, _) in enumerate(ROWS, start=1):
+            w.writerow(["KERNEL_DISPATCH", i, name, 256, 256, t, t + dur])
+            t += dur + 100
+
+
+def write_counters(path, counter, col):
+    with open(path, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Dispatch_Id", "Grid_Size", "Kernel_Name", "Workgroup_Size",
+                    "Counter_Name", "Counter_Value"])
+        for i, row in enumerate(ROWS, start=1):
+            w.writerow([i, 256, row[0], 256, counter, row[col]])
+
+
+@pytest.fixture()
+def files(tmp_path):
+    write_trace(tmp_path / "t.csv")
+    write_counters(tmp_path / "f.csv", "FETCH_SIZE", 2)
+    write_counters(tmp_path / "w.csv", "WRITE_SIZE", 3)
+    return tmp_path
+
+
+def test_summary_scales_counters_by_the_calibration_copy(files):
+    res = rocprof.summarize(MANIFEST, trace=rocprof.read_trace(files / "t.csv"),
+                            fetch=rocprof.read_counters(files / "f.csv"),
+                            write=rocprof.read_counters(files / "w.csv"))
+    # 1 MiB copy: FETCH reads 512 KiB -> x2, WRITE reads 1024 KiB -> x1.
+    assert res["FETCH_SIZE_scale"] == pytest.approx(2.0)
+    assert res["WRITE_SIZE_scale"] == pytest.approx(1.0)
+    g = res["workloads"]["gemv"]
+    assert g["call_us"] == pytest.approx(3.0)            # median of 2 and 4 (warm-up dropped)
+    assert g["fetch_bytes"] == pytest.approx(0.5 * 1024 * 2)
+    assert g["write_bytes"] == pytest.approx(0.25 * 1024)
+    assert g["traffic_bytes"] == pytest.approx(1024 + 256)
+    a = res["workloads"]["attn"]
+    assert a["call_us"] == pytest.approx(5.0)            # (3+1) and (5+1) -> median 5
+    assert a["kernel_us"]["void dbk::(anonymous namespace)::f4_combine"] == pytest.approx(1.0)
+    assert a["fetch_bytes"] == pytest.approx(2.5 * 1024 * 2)
+    assert a["GB/s"] == pytest.approx(5000 / 5000.0)
+    assert rocprof.short_name("void dbk::(anonymous namespace)::gemv_kernel<1, 8>"
+                              "(dbk::(anonymous namespace)::GemvArgs)") == \
+        "void dbk::(anonymous namespace)::gemv_kernel<1, 8>"
+    text = rocprof.to_markdown(res, "rocprofv3 ... -- python3 bench.py --profile-pass m.json")
+    assert "| attn |" in text and "bench.py --profile-pass" in text
+
+
+def test_mismatched_profile_fails(files):
+    bad = dict(MANIFEST, workloads=[dict(MANIFEST["workloads"][0], calls=4)] +
+               MANIFEST["workloads"][1:])
+    with pytest.raises(ValueError, match="manifest expects"):
+        rocprof.summarize(bad, trace=rocprof.read_trace(files / "t.csv"))
+    with pytest.raises(ValueError, match="calibration"):
+        rocprof.summarize(dict(MANIFEST, copy_calls=5),
+                          fetch=rocprof.read_counters(files / "f.csv"))
