@@ -20,10 +20,13 @@
 //    lands as S[key 4g+i][head n] in lane 16g+n, register i.
 //  * Online softmax runs in base 2 (scale * log2 e folded into the scores) on
 //    the 4 keys each lane holds; the tile max crosses rows with two lane
-//    swaps.  Probabilities reach the P.V lanes through DPP row_newbcast, since
-//    lane (r, c) of the P.V layout needs keys 4r..4r+3, which live in row r.
-//  * P.V is fp32 FMA on the VALU: lane (r, c) owns d = 8c..8c+7 of every head
-//    for the V rows 4r..4r+3 of each tile.
+//    swaps.  The fp16 probabilities are already the B operand (P^T) of the
+//    P.V product in the score accumulator's layout.
+//  * P.V is eight v_mfma_f32_16x16x16_f16 per tile (O^T = V^T P^T, one per 16
+//    dims of D).  Their A operand (V^T) comes from the wave's copy of the V
+//    tile in LDS through the gfx950 transposing read ds_read_b64_tr_b16, so
+//    the VALU does no per-key multiply-adds and the outputs need no
+//    cross-lane reduction at the end.
 //  * The waves merge through LDS.  With S = 1 the workgroup writes the fp16
 //    output.  With S > 1 splits each workgroup writes an unnormalised partial
 //    (o, and the pair (m, l) per head) and a second, small launch merges the
@@ -46,6 +49,12 @@ constexpr int kD = 128;
 constexpr int kTile = 16;
 constexpr int kPrefetch = 4;  // tiles loaded up front on the short path
 constexpr int kMergeChunk = 8;
+// Row stride (halves) of a V tile in LDS: 128 + 16 padding keeps the four
+// rows one transposed read touches in different banks.
+constexpr int kVStride = 144;
+
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef short s4 __attribute__((ext_vector_type(4)));
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
 
@@ -63,21 +72,6 @@ struct F4Args {
   float scale_log2;    // scale * log2(e)
 };
 
-template <int G>
-__device__ __forceinline__ float bcast_head(float v, int h) {
-  // h is a compile-time constant at every call site after unrolling.
-  switch (h) {
-    case 0: return row_bcast<0>(v);
-    case 1: return row_bcast<1>(v);
-    case 2: return row_bcast<2>(v);
-    case 3: return row_bcast<3>(v);
-    case 4: return row_bcast<4>(v);
-    case 5: return row_bcast<5>(v);
-    case 6: return row_bcast<6>(v);
-    default: return row_bcast<7>(v);
-  }
-}
-
 __device__ __forceinline__ float xor_lanes(float v, int m) {
   return __shfl_xor(v, m);
 }
@@ -92,6 +86,7 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
   static_assert(G >= 1 && G <= 8, "query heads per KV head");
   constexpr int kThreads = NW * kWave;
 
+  __shared__ __align__(16) _Float16 s_v[NW][kTile][kVStride];  // per-wave V tile
   __shared__ __align__(16) float s_o[NW][G][kD];  // per-wave outputs
   __shared__ float s_m[NW][G];
   __shared__ float s_l[NW][G];
@@ -132,11 +127,10 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
   const int nt = first < t_end ? (t_end - first + NW - 1) / NW : 0;
   const int last_row = a.L - 1;
 
-  float o[G][8];
+  // O^T accumulators: lane (g4, n16) holds O[head n16][16 b + 4 g4 + i].
+  f4 o[kD / 16];
 #pragma unroll
-  for (int h = 0; h < G; ++h)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[h][i] = 0.0f;
+  for (int b = 0; b < kD / 16; ++b) o[b] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   float m_run = kNegInf;  // per head n16 (uniform over g4)
   float l_run = 0.0f;     // partial over this lane's keys
 
@@ -153,7 +147,16 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
     }
   };
 
+  // V^T operands come from a per-wave row-major copy of the V tile in LDS,
+  // read back with ds_read_b64_tr_b16: lane 16g + 4r + q supplies the
+  // address of V[4g + r][d0 + 4q] and receives V[4g .. 4g+3][d0 + (lane & 15)],
+  // the A-operand layout of v_mfma_f32_16x16x16_f16 for O^T = V^T P^T.
+  _Float16* vbuf = &s_v[wave][0][0];
   auto compute_tile = [&](const u4 (&kt)[4], const u4 (&vt)[4], int tile) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<u4*>(vbuf + (4 * g4 + j) * kVStride + 8 * n16) = vt[j];
+
     f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -170,36 +173,29 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
     tmax = fmaxf(tmax, xor_lanes(tmax, 32));
     const float m_new = fmaxf(m_run, tmax);
     const float alpha = fast_exp2(m_run - m_new);
-    float p[4];
+    // P^T operand: lane (g4, n16) holds P[keys 4g4..4g4+3][head n16], the
+    // accumulator layout of the score MFMA.  p is rounded to fp16 for the
+    // product (as the reference stage rounds p before P.V) and the exp-sum
+    // adds the rounded values, so numerator and denominator agree.
+    h4 pb;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) p[i] = fast_exp2(s[i] - m_new);
-    l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+    for (int i = 0; i < 4; ++i) pb[i] = (_Float16)fast_exp2(s[i] - m_new);
+    l_run = l_run * alpha + (((float)pb[0] + (float)pb[1]) + ((float)pb[2] + (float)pb[3]));
     m_run = m_new;
 
-    // Rescale the running output only when some head's max moved.
+    // Rescale the running output only when some head's max moved; alpha of
+    // head n16 lives in the lanes that hold that head's outputs.
     if (__any(alpha != 1.0f)) {
 #pragma unroll
-      for (int h = 0; h < G; ++h) {
-        const float ah = bcast_head<G>(alpha, h);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[h][i] *= ah;
-      }
+      for (int b = 0; b < kD / 16; ++b) o[b] *= alpha;
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float vf[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const h2 pr = as_h2(vt[j][i]);
-        vf[2 * i] = (float)pr[0];
-        vf[2 * i + 1] = (float)pr[1];
-      }
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        const float ph = bcast_head<G>(p[j], h);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[h][i] = fmaf(ph, vf[i], o[h][i]);
-      }
+    for (int b = 0; b < kD / 16; ++b) {
+      const h4 va = __builtin_bit_cast(
+          h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                  (__attribute__((address_space(3))) s4*)(
+                      vbuf + (4 * g4 + (n16 >> 2)) * kVStride + 16 * b + 4 * (n16 & 3))));
+      o[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb, o[b], 0, 0, 0);
     }
   };
 
@@ -259,21 +255,10 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
     s_m[wave][lane] = m_run;
     s_l[wave][lane] = l_tot;
   }
-  // Sum the four row groups (g4) of the P.V layout: same d, disjoint keys.
+  if (n16 < G) {
 #pragma unroll
-  for (int h = 0; h < G; ++h)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      o[h][i] += xor_lanes(o[h][i], 16);
-      o[h][i] += xor_lanes(o[h][i], 32);
-    }
-  if (g4 == 0) {
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      float* dst = &s_o[wave][h][n16 * 8];
-      *reinterpret_cast<f4*>(dst) = f4{o[h][0], o[h][1], o[h][2], o[h][3]};
-      *reinterpret_cast<f4*>(dst + 4) = f4{o[h][4], o[h][5], o[h][6], o[h][7]};
-    }
+    for (int b = 0; b < kD / 16; ++b)
+      *reinterpret_cast<f4*>(&s_o[wave][n16][16 * b + 4 * g4]) = o[b];
   }
   __syncthreads();
 
@@ -378,15 +363,13 @@ __global__ __launch_bounds__(256) void f4_combine(F4Args a, int G) {
 
 using F4Fn = void (*)(F4Args);
 
-// Eight-wave workgroups exist for G <= 4 only: with G = 8 the per-lane
-// output accumulators do not fit the 256 registers a 512-thread workgroup
-// leaves each wave.
 F4Fn pick_kernel(int G, int waves) {
   if (waves == 8) {
     switch (G) {
       case 1: return f4_kernel<1, 8>;
       case 2: return f4_kernel<2, 8>;
-      default: return f4_kernel<4, 8>;
+      case 4: return f4_kernel<4, 8>;
+      default: return f4_kernel<8, 8>;
     }
   }
   switch (G) {
@@ -454,7 +437,6 @@ hipError_t launch_f4(const void* q, const void* k, const void* v, void* o,
   a.scale_log2 = scale * kLog2e;
   (void)D;
   int waves = tuning().f4_waves > 0 ? tuning().f4_waves : (a.tps >= 16 ? 8 : 4);
-  if (G == 8) waves = 4;
   hipLaunchKernelGGL(pick_kernel(G, waves), dim3(pairs * a.S), dim3(waves * kWave), 0,
                      stream, a);
   if (a.S > 1) {
