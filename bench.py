@@ -30,6 +30,7 @@ import json
 import math
 import os
 import platform
+import re
 import sys
 import time
 
@@ -38,6 +39,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0   # dense fp16 MFMA, MI355X
 METRIC = ("fused kernel µs + HBM GB/s (% of ~8 TB/s) for F1/F2/F4 at bs=1; "
           "Δ_launch vs B")
 
@@ -61,6 +63,9 @@ def parse_args(argv=None):
     ap.add_argument("--profile-pass", metavar="MANIFEST",
                     help="run the workload for rocprofv3 instead: calibration copies, then "
                          "every kernel eagerly; write the launch manifest to MANIFEST and exit")
+    ap.add_argument("--sweep-only", metavar="REGEX",
+                    help="per-kernel table restricted to matching workloads; skips the "
+                         "decomposition and the CPU baseline")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.json"),
                     help="rocprofv3 traffic summary (decodebench_amd.rocprof) for roofline.traffic")
     return ap.parse_args(argv)
@@ -141,10 +146,27 @@ def check_case(case) -> float:
 
 def kernel_row(case, us: float) -> dict:
     gbs = case.algorithmic_bytes / (us * 1e-6) / 1e9
+    tflops = case.flops / (us * 1e-6) / 1e12
     return {"us": round(us, 3), "GB/s": round(gbs, 1),
             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
-            "algorithmic_bytes": case.algorithmic_bytes,
+            "TFLOP/s": round(tflops, 2), "frac_mfma_f16": round(tflops / MFMA_F16_PEAK_TFLOPS, 5),
+            "algorithmic_bytes": case.algorithmic_bytes, "flops": case.flops,
             "replicas": len(case.replicas), "shape": case.shape}
+
+
+def sweep_workloads():
+    """BASELINE configs 1-4 with their batch, KV-length and split sweeps."""
+    out = [("f1_cfg1", dict(name="f1", batch=1))]
+    for B in (1, 4, 8, 16, 32):
+        out.append((f"f1_qkv_cfg3" + ("" if B == 1 else f"_B{B}"), dict(name="f1_qkv", batch=B)))
+    for B in (1, 4, 16):
+        out.append((f"f2_cfg2" + ("" if B == 1 else f"_B{B}"), dict(name="f2", batch=B)))
+    for L in (1024, 8192, 32768):
+        for B in (1, 4, 8):
+            out.append((f"f4_L{L}" + ("" if B == 1 else f"_B{B}"), dict(name="f4", L=L, batch=B)))
+    for S in (1, 4, 16, 64):
+        out.append((f"f4_L8192_S{S}", dict(name="f4", L=8192, batch=1, n_splits=S)))
+    return out
 
 
 # ------------------------------------------------------------ profile pass
@@ -309,22 +331,22 @@ def main(argv=None) -> int:
     if not args.quick:
         # ---- per-kernel table (graph-replayed back-to-back launches) -----
         kernels = {}
-        for name, kw in (("f1_cfg1", dict(name="f1")), ("f1_qkv_cfg3", dict(name="f1_qkv")),
-                         ("f2_cfg2", dict(name="f2")),
-                         ("f4_L1024", dict(name="f4", L=1024)),
-                         ("f4_L8192", dict(name="f4", L=8192)),
-                         ("f4_L32768", dict(name="f4", L=32768))):
-            case = build_config(batch=1, **kw)
+        for name, kw in sweep_workloads():
+            if args.sweep_only and not re.search(args.sweep_only, name):
+                continue
+            case = build_config(gen_device="cuda", **kw)
             check_case(case)
             us_k, launches = time_graph_launches(case)
             kernels[name] = kernel_row(case, us_k)
             kernels[name]["launches_per_graph"] = launches
             kernels[name]["traffic_bytes"] = traffic.get(name, {}).get("traffic_bytes")
-            log(f"{name}: {us_k:.2f} us, {kernels[name]['GB/s']:.0f} GB/s")
+            log(f"{name}: {us_k:.2f} us, {kernels[name]['GB/s']:.0f} GB/s, "
+                f"{kernels[name]['TFLOP/s']:.1f} TFLOP/s")
             del case
             torch.cuda.empty_cache()
         out["kernels"] = kernels
 
+    if not args.quick and not args.sweep_only:
         # ---- Delta_launch vs B: unfused stream / graph vs fused ----------
         decomp = {}
         for name, kw in (("f1_cfg1", dict(name="f1")), ("f2_cfg2", dict(name="f2")),

@@ -10,6 +10,7 @@ namespace dbk {
 // changed at run time through db_tune() for launch-shape sweeps.
 struct Tuning {
   int gemv_waves_per_cu = 0;   // 0: choose from the row-group count
+  int gemv_mfma_min_batch = 2; // smallest batch that takes the MFMA GEMV
   int f4_blocks_per_cu = 1;    // target F4 workgroups per CU
   int f4_min_tiles = 2;        // minimum 16-row tiles per F4 split
   int f4_waves = 0;            // waves per F4 workgroup (4 or 8; 0: auto)
@@ -28,6 +29,12 @@ enum GemvMode : int { kGemvPlain = 0, kGemvRmsNorm = 1, kGemvSwiGLU = 2 };
 hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
                        const void* w0, const void* w1, void* y, int B, int K,
                        int N, float eps, int cu_count, hipStream_t stream);
+
+// MFMA variant for batches of 2..16 rows per pass (gemv_mfma.hip).
+bool gemv_mfma_supported(int B, int K, int N);
+hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
+                            const void* w0, const void* w1, void* y, int B, int K,
+                            int N, float eps, int cu_count, hipStream_t stream);
 
 // Split-KV GQA decode attention with the log-sum-exp combine in-kernel.
 size_t f4_workspace_bytes(int B, int Hq, int Hkv, int S, int D);

@@ -351,6 +351,8 @@ hipError_t allow_large_lds(const void* fn) {
 hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
                        const void* w0, const void* w1, void* y, int B, int K,
                        int N, float eps, int cu_count, hipStream_t stream) {
+  if (B >= tuning().gemv_mfma_min_batch && gemv_mfma_supported(B, K, N))
+    return launch_gemv_mfma(mode, x, gamma, w0, w1, y, B, K, N, eps, cu_count, stream);
   const int R = rows_per_group(mode);
   GemvArgs a;
   a.x = static_cast<const _Float16*>(x);

@@ -1,0 +1,343 @@
+// gemv_mfma.hip -- batched decode GEMV on MFMA (batch 2..16 per pass) for gfx950.
+//
+// y[B,N] = op(x[B,K]) . W^T for the three GEMV modes of gemv.hip (plain,
+// RMSNorm-fused F1, gate/up + SwiGLU F2) when the batch is large enough that
+// the VALU dot-product path becomes instruction-bound (at batch 8 it runs at
+// a third of HBM speed).  The weights are still read exactly once; MFMA does
+// the multiply-adds.
+//
+// Decomposition
+//  * One persistent workgroup per CU, 8 waves.  Wave v owns K-slice v
+//    (K / 8 columns) of every weight row, split into halves h = 0, 1.
+//  * Weight rows are taken in groups of 8, which spreads N / 8 groups evenly
+//    over the CUs at N = 4096, 6144 and 14336.  One v_mfma_f32_16x16x32_f16
+//    covers 8 rows x both halves: A-operand rows 0..7 are the group's rows
+//    over half 0 and rows 8..15 the same rows over half 1; B-operand columns
+//    0..7 are 8 batch rows over half 0 and columns 8..15 the same batch rows
+//    over half 1.  D[m][n] + D[m+8][n+8] is then the slice's dot product of
+//    weight row m and batch row n (the off-diagonal quarters are dropped),
+//    and every loaded weight byte is used.
+//  * The activation slice of up to 16 batch rows (two column tiles of 8)
+//    stays in registers for the whole kernel in that B-operand layout;
+//    lane (g, n) holds x[b][k0 + 32 t + 8 g .. + 7] of its half.
+//  * Workgroup w owns groups w, w + grid, ...; each wave streams its slice of
+//    them with 16-byte loads.  When they fit in registers (up to 4 groups of
+//    one matrix or 2 of the gate/up pair) all are requested before the
+//    prologue; otherwise two register sets alternate (load set B, consume A,
+//    reload A, consume B).
+//  * Each wave's partial sums (8 rows x 16 batch per group) go to LDS; after
+//    the last group the workgroup reduces the 8 K-slices and applies the
+//    epilogue (fp16 rounding, or SiLU(g) * u with the reference's rounding
+//    points), storing only the final fp16 outputs.
+//  * F1: each wave sums x^2 over its slice, the 8 partial sums meet in LDS,
+//    and every wave normalises its own x registers exactly as the torch stage
+//    rounds: fp16(fp16(x * inv_rms) * gamma), gamma read from an LDS copy.
+// Batches above 16 run as passes of 16 (grid.y); each pass re-reads the
+// weights.
+#include "db_device.h"
+#include "db_kernels.h"
+
+namespace dbk {
+
+namespace {
+
+constexpr int kWavesM = 8;
+constexpr int kThreadsM = kWavesM * kWave;
+constexpr int kRowsPerGroup = 8;
+constexpr int kBatchTile = 16;
+constexpr int kMaxGroupsPerWg = 8;   // LDS partial-sum slots per workgroup
+
+struct MfmaArgs {
+  const _Float16* x;      // [B, K]
+  const _Float16* gamma;  // [K]     (RMSNorm mode)
+  const _Float16* w0;     // [N, K]  (gate in SwiGLU mode)
+  const _Float16* w1;     // [N, K]  (up, SwiGLU mode only)
+  _Float16* y;            // [B, N]
+  int B, K, N;
+  int groups;             // ceil(N / 8)
+  int gpw;                // groups per workgroup (<= kMaxGroupsPerWg)
+  float eps;
+};
+
+__device__ __forceinline__ float silu_m(float g) { return g / (1.0f + __expf(-g)); }
+
+// KH: k-steps (32 columns each) per half slice, K / 512.
+// BT: batch column tiles of 8 (1 for batch <= 8, 2 for <= 16).
+// UPS: groups per register set.  When a workgroup's groups fit in one set
+// (UPS >= groups per workgroup) they are all requested before the prologue
+// and no loop runs; otherwise two sets alternate.
+template <int MODE, int KH, int BT, int UPS, bool SINGLE>
+__global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
+  constexpr int NWM = (MODE == kGemvSwiGLU) ? 2 : 1;
+  // [group][matrix][wave][batch][row]
+  __shared__ __align__(16) float part[kMaxGroupsPerWg][NWM][kWavesM][kBatchTile][kRowsPerGroup];
+  __shared__ float red[kWavesM][kBatchTile];
+  __shared__ u4 s_gamma[MODE == kGemvRmsNorm ? kThreadsM : 1];  // K / 8 chunks
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int c16 = lane & 15;  // A row m / B column n
+  const int g4 = lane >> 4;   // k-group
+  const int r8 = c16 & 7;     // weight row in the group / batch row in the tile
+  const int half = c16 >> 3;  // which half of the slice this lane covers
+  const int b0 = blockIdx.y * kBatchTile;
+  const int nb = min(kBatchTile, a.B - b0);
+  // This lane's first column: the slice of wave v is [v, v+1) * K / 8.
+  const int kcol = wave * KH * 64 + half * KH * 32 + 8 * g4;
+
+  // ---- activation slice -> registers (B operand), loads unconditional ----
+  // F1's gamma is shared by every batch row: thread t fetches 16-byte chunk t
+  // (K / 8 <= 512 chunks) for the LDS copy the normalisation reads.  Both
+  // are issued before the first weight loads, so waiting for them never
+  // waits for weights (loads complete in issue order).
+  u4 xr[BT][KH];
+#pragma unroll
+  for (int bt = 0; bt < BT; ++bt) {
+    const int xrow = b0 + min(8 * bt + r8, nb - 1);
+#pragma unroll
+    for (int t = 0; t < KH; ++t) xr[bt][t] = ld16(a.x + (size_t)xrow * a.K + kcol + 32 * t);
+  }
+  u4 gchunk = {0, 0, 0, 0};
+  if constexpr (MODE == kGemvRmsNorm)
+    gchunk = ld16(a.gamma + 8 * min((int)threadIdx.x, a.K / 8 - 1));
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- the workgroup's groups: rows of group j are 8 (w + grid j) .. +7 --
+  const int my_groups = min(a.gpw, (a.groups - (int)blockIdx.x + (int)gridDim.x - 1) /
+                                       (int)gridDim.x);
+  const _Float16* wmat[2] = {a.w0, a.w1};
+  // `checked`: skip groups past my_groups (only outside the steady loop,
+  // whose loads are unconditional so the compiler waits per set).
+  auto load_set = [&](u4 (&dst)[UPS][NWM][KH], int j0, bool checked) {
+#pragma unroll
+    for (int q = 0; q < UPS; ++q) {
+      if (checked && j0 + q >= my_groups) break;
+      const int grp = blockIdx.x + gridDim.x * min(j0 + q, my_groups - 1);
+      const int row = min(grp * kRowsPerGroup + r8, a.N - 1);
+#pragma unroll
+      for (int m = 0; m < NWM; ++m)
+#pragma unroll
+        for (int t = 0; t < KH; ++t)
+          dst[q][m][t] = ld_stream(wmat[m] + (size_t)row * a.K + kcol + 32 * t);
+    }
+  };
+
+  u4 wa[UPS][NWM][KH];
+  load_set(wa, 0, true);  // every workgroup owns at least one group
+  __builtin_amdgcn_sched_barrier(0);
+
+  const u4 zero4 = {0, 0, 0, 0};
+#pragma unroll
+  for (int bt = 0; bt < BT; ++bt) {
+    const bool valid = 8 * bt + r8 < nb;
+#pragma unroll
+    for (int t = 0; t < KH; ++t) xr[bt][t] = valid ? xr[bt][t] : zero4;
+  }
+
+  if constexpr (MODE == kGemvRmsNorm) {
+    // x^2 over this slice per batch row: in-lane, then over the two halves
+    // (lanes 8 apart) and the 4 k-groups (lanes 16 apart).
+    float ss[BT];
+#pragma unroll
+    for (int bt = 0; bt < BT; ++bt) {
+      ss[bt] = 0.0f;
+#pragma unroll
+      for (int t = 0; t < KH; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const h2 p = as_h2(xr[bt][t][j]);
+          const float lo = (float)p[0], hi = (float)p[1];
+          ss[bt] += lo * lo + hi * hi;
+        }
+      ss[bt] += __shfl_xor(ss[bt], 8);
+      ss[bt] += __shfl_xor(ss[bt], 16);
+      ss[bt] += __shfl_xor(ss[bt], 32);
+      if (lane < 8) red[wave][8 * bt + lane] = ss[bt];
+    }
+    if ((int)threadIdx.x < a.K / 8) s_gamma[threadIdx.x] = gchunk;
+    __syncthreads();
+#pragma unroll
+    for (int bt = 0; bt < BT; ++bt) {
+      float tot = 0.0f;
+#pragma unroll
+      for (int v = 0; v < kWavesM; ++v) tot += red[v][8 * bt + r8];
+      const float inv = 1.0f / sqrtf(tot / (float)a.K + a.eps);
+#pragma unroll
+      for (int t = 0; t < KH; ++t) {
+        const u4 gv = s_gamma[(kcol + 32 * t) / 8];
+        u4 out;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const h2 xp = as_h2(xr[bt][t][j]);
+          const h2 gp = as_h2(gv[j]);
+          const float n0 = (float)to_h((float)xp[0] * inv);
+          const float n1 = (float)to_h((float)xp[1] * inv);
+          out[j] = pack_h2(n0 * (float)gp[0], n1 * (float)gp[1]);
+        }
+        xr[bt][t] = out;
+      }
+    }
+  }
+
+  // ---- stream the groups ------------------------------------------------
+  auto consume = [&](const u4 (&src)[UPS][NWM][KH], int j0) {
+#pragma unroll
+    for (int q = 0; q < UPS; ++q) {
+      const int j = j0 + q;
+      if (j >= my_groups) break;
+#pragma unroll
+      for (int m = 0; m < NWM; ++m) {
+#pragma unroll
+        for (int bt = 0; bt < BT; ++bt) {
+          f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int t = 0; t < KH; ++t)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, src[q][m][t]),
+                                                         __builtin_bit_cast(h8, xr[bt][t]), acc,
+                                                         0, 0, 0);
+          // D[4 g4 + i][c16]: rows 0..7 x columns 0..7 (half 0) live in lanes
+          // (g4 < 2, c16 < 8); their half-1 partners sit 40 lanes higher.
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i] += __shfl(acc[i], lane + 40);
+          if (g4 < 2 && c16 < 8)
+            *reinterpret_cast<f4*>(&part[j][m][wave][8 * bt + c16][4 * g4]) = acc;
+        }
+      }
+    }
+  };
+
+  if constexpr (SINGLE) {
+    consume(wa, 0);  // every group of the workgroup is in set A
+  } else {
+    // Two register sets; the steady loop loads and consumes set B inside
+    // one iteration (see flashdecode.hip for why that matters to the
+    // compiler).
+    u4 wb[UPS][NWM][KH];
+    int j = 0;
+    for (; j + 3 * UPS <= my_groups; j += 2 * UPS) {
+      load_set(wb, j + UPS, false);
+      consume(wa, j);
+      load_set(wa, j + 2 * UPS, false);
+      consume(wb, j + UPS);
+    }
+    // Fewer than 3 * UPS groups remain; set A holds the first UPS of them.
+    if (j + UPS < my_groups) load_set(wb, j + UPS, true);
+    consume(wa, j);
+    if (j + 2 * UPS < my_groups) load_set(wa, j + 2 * UPS, true);
+    if (j + UPS < my_groups) consume(wb, j + UPS);
+    if (j + 2 * UPS < my_groups) consume(wa, j + 2 * UPS);
+  }
+
+  __syncthreads();
+
+  // ---- reduce the 8 K-slices, epilogue, fp16 store ----------------------
+  const int nout = my_groups * kBatchTile * kRowsPerGroup;
+  for (int idx = threadIdx.x; idx < nout; idx += kThreadsM) {
+    const int jj = idx / (kBatchTile * kRowsPerGroup);
+    const int n = (idx / kRowsPerGroup) % kBatchTile;
+    const int r = idx % kRowsPerGroup;
+    const int row = (blockIdx.x + gridDim.x * jj) * kRowsPerGroup + r;
+    if (n >= nb || row >= a.N) continue;
+    float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+    for (int v = 0; v < kWavesM; ++v) {
+      s0 += part[jj][0][v][n][r];
+      if constexpr (NWM == 2) s1 += part[jj][NWM - 1][v][n][r];
+    }
+    float out;
+    if constexpr (MODE == kGemvSwiGLU) {
+      const float gq = (float)to_h(s0);
+      const float uq = (float)to_h(s1);
+      out = (float)to_h(silu_m(gq)) * uq;
+    } else {
+      out = s0;
+    }
+    a.y[(size_t)(b0 + n) * a.N + row] = to_h(out);
+  }
+}
+
+using MfmaFn = void (*)(MfmaArgs);
+
+// ups > 0: one set of `ups` groups holds all of a workgroup's groups;
+// ups < 0: alternating sets of -ups groups.
+template <int MODE, int KH, int BT>
+MfmaFn pick_ups(int ups) {
+  if constexpr (MODE == kGemvSwiGLU) {
+    return ups == 2 ? gemv_mfma_kernel<MODE, KH, BT, 2, true>
+                    : gemv_mfma_kernel<MODE, KH, BT, 1, false>;
+  } else if constexpr (MODE == kGemvRmsNorm && BT == 2) {
+    // Two batch tiles of F1 leave no registers for a whole-workgroup set
+    // next to the normalisation; always alternate two sets of 2 groups.
+    (void)ups;
+    return gemv_mfma_kernel<MODE, KH, BT, 2, false>;
+  } else {
+    switch (ups) {
+      case 2: return gemv_mfma_kernel<MODE, KH, BT, 2, true>;
+      case 3: return gemv_mfma_kernel<MODE, KH, BT, 3, true>;
+      case 4: return gemv_mfma_kernel<MODE, KH, BT, 4, true>;
+      default: return gemv_mfma_kernel<MODE, KH, BT, 2, false>;
+    }
+  }
+}
+
+template <int MODE, int KH>
+MfmaFn pick_bt(int bt, int ups) {
+  return bt == 1 ? pick_ups<MODE, KH, 1>(ups) : pick_ups<MODE, KH, 2>(ups);
+}
+
+template <int MODE>
+MfmaFn pick_kh(int kh, int bt, int ups) {
+  return kh == 4 ? pick_bt<MODE, 4>(bt, ups) : pick_bt<MODE, 8>(bt, ups);
+}
+
+// Register sets: everything at once when it fits (up to 4 groups of one
+// matrix, 2 of the gate/up pair, at 8 or 16 loads per group and matrix),
+// else alternating sets of 2 groups (1 for the pair).  See pick_ups.
+int pick_sets(GemvMode mode, int gpw) {
+  if (mode == kGemvSwiGLU) return gpw <= 2 ? 2 : -1;
+  return gpw <= 2 ? 2 : (gpw <= 4 ? gpw : -2);
+}
+
+}  // namespace
+
+bool gemv_mfma_supported(int B, int K, int N) {
+  if (B < 2 || N < 1) return false;
+  if (K != 2048 && K != 4096) return false;  // K / 512 = 4 or 8 k-steps per half
+  const int groups = (N + kRowsPerGroup - 1) / kRowsPerGroup;
+  return groups <= 256 * kMaxGroupsPerWg;
+}
+
+hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
+                            const void* w0, const void* w1, void* y, int B, int K,
+                            int N, float eps, int cu_count, hipStream_t stream) {
+  MfmaArgs a;
+  a.x = static_cast<const _Float16*>(x);
+  a.gamma = static_cast<const _Float16*>(gamma);
+  a.w0 = static_cast<const _Float16*>(w0);
+  a.w1 = static_cast<const _Float16*>(w1);
+  a.y = static_cast<_Float16*>(y);
+  a.B = B;
+  a.K = K;
+  a.N = N;
+  a.eps = eps;
+  a.groups = (N + kRowsPerGroup - 1) / kRowsPerGroup;
+  int grid = min(a.groups, cu_count);
+  a.gpw = (a.groups + grid - 1) / grid;
+  if (a.gpw > kMaxGroupsPerWg) a.gpw = kMaxGroupsPerWg;
+  // Spread the groups evenly: every workgroup owns gpw or gpw - 1 groups.
+  grid = (a.groups + a.gpw - 1) / a.gpw;
+  const int kh = K / 512;
+  const int bt = B >= 9 ? 2 : 1;  // batch column tiles of the 16-row pass
+  const int ups = pick_sets(mode, a.gpw);
+  MfmaFn fn;
+  switch (mode) {
+    case kGemvRmsNorm: fn = pick_kh<kGemvRmsNorm>(kh, bt, ups); break;
+    case kGemvSwiGLU: fn = pick_kh<kGemvSwiGLU>(kh, bt, ups); break;
+    default: fn = pick_kh<kGemvPlain>(kh, bt, ups); break;
+  }
+  dim3 g(grid, (B + kBatchTile - 1) / kBatchTile);
+  hipLaunchKernelGGL(fn, g, dim3(kThreadsM), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace dbk

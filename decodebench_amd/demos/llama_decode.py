@@ -42,9 +42,12 @@ _HEAD_DIM = 128
 
 # ----------------------------------------------------------- random inputs
 def _randn(gen, shape, std: float = 1.0, mean: float = 0.0, device="cuda"):
+    """Seeded normal fp16 tensor on ``device``.  Drawn on the generator's own
+    device: a CPU generator gives values identical on every machine, a GPU
+    generator is fast for the large KV caches of benchmark sweeps."""
     import torch
 
-    t = torch.randn(*shape, generator=gen, dtype=torch.float32)
+    t = torch.randn(*shape, generator=gen, dtype=torch.float32, device=gen.device)
     if std != 1.0:
         t.mul_(std)
     if mean != 0.0:
@@ -207,13 +210,16 @@ def _replicate(inputs: dict, big: tuple[str, ...], n: int) -> list[dict]:
 
 def build_config(name: str, batch: int = 1, L: int = 8192, n_splits: int | None = None,
                  seed: int = 42, device="cuda", replicas: int | None = None,
-                 K: int = 4096) -> Case:
-    """BASELINE-shaped case; ``replicas=None`` sizes a cache-defeating rotation."""
+                 K: int = 4096, gen_device: str = "cpu") -> Case:
+    """BASELINE-shaped case; ``replicas=None`` sizes a cache-defeating rotation.
+
+    ``gen_device="cpu"`` draws the inputs on the CPU (device-independent
+    values, what the parity tests use); ``"cuda"`` draws them on the GPU."""
     import torch
 
     from decodebench_amd import ops
 
-    gen = torch.Generator().manual_seed(seed)
+    gen = torch.Generator(device=gen_device).manual_seed(seed)
     B = batch
     if name in ("f1", "f1_qkv"):
         N = 4096 if name == "f1" else 6144

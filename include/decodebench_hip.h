@@ -118,7 +118,7 @@ int db_f4_splitkv(const void* q, const void* k, const void* v, void* o,
                   int D, int S, float scale, void* stream);
 
 /* Launch-geometry knobs for tuning sweeps ("gemv_waves_per_cu",
- * "f4_blocks_per_cu", "f4_min_tiles", "f4_waves"); value <= 0 restores the
+ * "gemv_mfma_min_batch", "f4_blocks_per_cu", "f4_min_tiles", "f4_waves"); value <= 0 restores the
  * default for the GEMV knob, 0 for "f4_waves" (4 or 8 waves per workgroup).
  * No counterpart in the reference. */
 int db_tune(const char* key, int value);

@@ -122,6 +122,63 @@ def test_plain_gemv_parity():
     assert_parity(y, ref, exact, F12_REL_L2, "gemv 2x14336x4096")
 
 
+# --------------------------------------------------- batched GEMV (MFMA)
+# Batches of 2 and more with K in {2048, 4096} take the MFMA kernel: ragged
+# batches (one and two 16-row passes), N not a multiple of the 8-row group.
+MFMA_CASES = [
+    ("f1", 2, 4096, 1000), ("f1", 17, 4096, 6144), ("f1", 32, 2048, 1032),
+    ("f2", 4, 4096, 14336), ("f2", 32, 4096, 1792), ("f2", 9, 2048, 777),
+    ("plain", 16, 4096, 4100), ("plain", 3, 2048, 8),
+]
+
+
+@pytest.mark.parametrize("mode,B,K,N", MFMA_CASES)
+def test_batched_gemv_mfma_parity(mode, B, K, N):
+    print(f"[mfma] {mode} B={B} K={K} N={N}", flush=True)
+    gen = torch.Generator().manual_seed(4000 + B + K + N)
+    x = randn(gen, (B, K))
+    if mode == "f1":
+        g = randn(gen, (K,), std=0.1, mean=1.0)
+        W = randn(gen, (N, K), std=0.02)
+        y = ops.f1_rmsnorm_gemv(x.cuda(), g.cuda(), W.cuda())
+        ref, exact, bound = stages.f1(x, g, W), cref.f1_exact(x.numpy(), g.numpy(), W.numpy()), \
+            F12_REL_L2
+    elif mode == "f2":
+        Wg = randn(gen, (N, K), std=0.02)
+        Wu = randn(gen, (N, K), std=0.02)
+        y = ops.f2_gateup_swiglu(x.cuda(), Wg.cuda(), Wu.cuda())
+        ref, exact, bound = stages.f2(x, Wg, Wu), \
+            cref.f2_exact(x.numpy(), Wg.numpy(), Wu.numpy()), 5e-3
+    else:
+        W = randn(gen, (N, K), std=0.02)
+        y = ops.gemv(x.cuda(), W.cuda())
+        ref, exact, bound = stages.gemv(x, W), cref.gemv_exact(x.numpy(), W.numpy()), F12_REL_L2
+    torch.cuda.synchronize()
+    assert y.shape == (B, N)
+    assert_parity(y, ref, exact, bound, f"{mode} B={B} K={K} N={N}")
+
+
+def test_mfma_and_valu_gemv_paths_agree():
+    """The same batch through both kernels (the MFMA threshold raised to force
+    the VALU path) differs only by fp32 summation order."""
+    gen = torch.Generator().manual_seed(77)
+    x = randn(gen, (8, 4096)).cuda()
+    g = randn(gen, (4096,), std=0.1, mean=1.0).cuda()
+    W = randn(gen, (6144, 4096), std=0.02).cuda()
+    Wu = randn(gen, (6144, 4096), std=0.02).cuda()
+    lib = ops.load_library()
+    try:
+        outs = []
+        for thr in (2, 1 << 20):
+            assert lib.db_tune(b"gemv_mfma_min_batch", thr) == 0
+            outs.append((ops.f1_rmsnorm_gemv(x, g, W), ops.f2_gateup_swiglu(x, W, Wu),
+                         ops.gemv(x, W)))
+    finally:
+        lib.db_tune(b"gemv_mfma_min_batch", 2)
+    for a, b in zip(*outs):
+        assert rel_l2(a.float().cpu().numpy(), b.float().cpu().numpy()) < 1e-3
+
+
 # ------------------------------------------------------------------- F4
 def f4_inputs(B, Hq, Hkv, L, seed):
     gen = torch.Generator().manual_seed(seed)
