@@ -12,11 +12,14 @@ the 256 MB Infinity Cache), so every step streams its weights from HBM.
   roofline       the F2 kernel against the 8 TB/s HBM3E peak; its average
                  launch duration is the same event-timed region on the
                  stream the kernel runs on (torch's current stream)
-  kernels        F1 (config 1 and the QKV shape of config 3) and F4
-                 (config 4 at L = 1024 / 8192 / 32768) at batch 1, each timed
-                 as back-to-back launches replayed from a hipGraph
+  kernels        F1 (config 1 and the QKV shape of config 3), F2 and F4
+                 (config 4 at L = 1024 / 8192 / 32768) with their batch and
+                 split sweeps, the fp8 e4m3-weight F1/F2 and the config-5
+                 decode layer (fp16 and fp8), each timed as back-to-back
+                 calls replayed from a hipGraph
   decomposition  Sequence.profile of the unfused torch stages (stream and
-                 graph) against the fused kernel: Delta_launch and B
+                 graph) against the fused kernels: Delta_launch and B, for
+                 F1, F2, F4 and the decode layer (fp16 and fp8 weights)
   cpu_baseline   the torch CPU restatement of the reference stages
                  (oracle/stages.py) on this host's cores, F2 at full size
 
@@ -166,13 +169,40 @@ def sweep_workloads():
             out.append((f"f4_L{L}" + ("" if B == 1 else f"_B{B}"), dict(name="f4", L=L, batch=B)))
     for S in (1, 4, 16, 64):
         out.append((f"f4_L8192_S{S}", dict(name="f4", L=8192, batch=1, n_splits=S)))
+    # fp8 e4m3 weights (per-row scales) at batch 1, and the config-5 layer
+    out += [("f1_cfg1_fp8", dict(name="f1", batch=1, dtype="fp8")),
+            ("f1_qkv_cfg3_fp8", dict(name="f1_qkv", batch=1, dtype="fp8")),
+            ("f2_cfg2_fp8", dict(name="f2", batch=1, dtype="fp8")),
+            ("layer_cfg5", dict(name="layer", batch=1, L=8192)),
+            ("layer_cfg5_fp8", dict(name="layer", batch=1, L=8192, dtype="fp8"))]
     return out
 
 
 # ------------------------------------------------------------ profile pass
 PROFILE_WORKLOADS = (("f1_cfg1", dict(name="f1")), ("f1_qkv_cfg3", dict(name="f1_qkv")),
                      ("f2_cfg2", dict(name="f2")), ("f4_L1024", dict(name="f4", L=1024)),
-                     ("f4_L8192", dict(name="f4", L=8192)), ("f4_L32768", dict(name="f4", L=32768)))
+                     ("f4_L8192", dict(name="f4", L=8192)), ("f4_L32768", dict(name="f4", L=32768)),
+                     ("f1_cfg1_fp8", dict(name="f1", dtype="fp8")),
+                     ("f1_qkv_cfg3_fp8", dict(name="f1_qkv", dtype="fp8")),
+                     ("f2_cfg2_fp8", dict(name="f2", dtype="fp8")),
+                     ("layer_cfg5", dict(name="layer", L=8192)),
+                     ("layer_cfg5_fp8", dict(name="layer", L=8192, dtype="fp8")))
+
+
+def kernels_per_call(kw: dict) -> int:
+    """Kernel launches of one fused call (F4 with S > 1 is two launches; the
+    decode layer is F1, F4, O GEMV, RMSNorm+F2 and the down GEMV)."""
+    from decodebench_amd import ops
+
+    def f4_launches(L):
+        return 2 if ops.f4_default_splits(1, 8, L) > 1 else 1
+
+    if kw["name"] == "f4":
+        return f4_launches(kw.get("L", 8192)) if kw.get("n_splits") is None else \
+            (2 if kw["n_splits"] > 1 else 1)
+    if kw["name"] == "layer":
+        return 4 + f4_launches(kw.get("L", 8192))
+    return 1
 
 
 def profile_pass(manifest_path: str, calls: int = 24, warmup: int = 4) -> int:
@@ -194,11 +224,8 @@ def profile_pass(manifest_path: str, calls: int = 24, warmup: int = 4) -> int:
     del src, dst
     workloads = []
     for label, kw in PROFILE_WORKLOADS:
-        case = build_config(batch=1, **kw)
-        per_call = 1
-        if kw["name"] == "f4":
-            s = case.shape["S"] or ops.f4_default_splits(1, case.shape["Hkv"], case.shape["L"])
-            per_call = 2 if s > 1 else 1
+        case = build_config(batch=1, gen_device="cuda", **kw)
+        per_call = kernels_per_call(kw)
         n = len(case.replicas)
         for i in range(calls):
             case.fused(case.replicas[i % n])
@@ -350,8 +377,10 @@ def main(argv=None) -> int:
         # ---- Delta_launch vs B: unfused stream / graph vs fused ----------
         decomp = {}
         for name, kw in (("f1_cfg1", dict(name="f1")), ("f2_cfg2", dict(name="f2")),
-                         ("f4_L8192", dict(name="f4", L=8192))):
-            case = build_config(batch=1, **kw)
+                         ("f4_L8192", dict(name="f4", L=8192)),
+                         ("layer_cfg5", dict(name="layer", L=8192)),
+                         ("layer_cfg5_fp8", dict(name="layer", L=8192, dtype="fp8"))):
+            case = build_config(batch=1, gen_device="cuda", **kw)
             rep = case.seq.profile(case.inputs, trials=args.trials, target_ms=10.0,
                                    warmup=10, input_replicas=case.replicas,
                                    fused=case.fused)

@@ -79,10 +79,15 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 // per CU; keep 8 KB for static arrays).
 constexpr size_t kGemvLdsBudget = 152 * 1024;
 
+bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+
+// Common GEMV contract.  W2/scale2 belong to the second matrix of the SwiGLU
+// entry points (NULL otherwise; `pair` says whether one is expected).
 int check_gemv(const char* fn, const void* x, const void* W, const void* y,
                int B, int K, int N, int w_dtype, const void* scale,
-               const void* W2, const void* scale2) {
-  if (!x || !W || !y) return fail(DB_ERR_INVALID, "%s: null tensor pointer", fn);
+               const void* W2, const void* scale2, bool pair) {
+  if (!x || !W || !y || (pair && !W2))
+    return fail(DB_ERR_INVALID, "%s: null tensor pointer", fn);
   if (B < 1 || N < 1 || K < 8)
     return fail(DB_ERR_INVALID, "%s: need B >= 1, N >= 1, K >= 8 (got B=%d K=%d N=%d)",
                 fn, B, K, N);
@@ -95,11 +100,39 @@ int check_gemv(const char* fn, const void* x, const void* W, const void* y,
     if (scale || scale2)
       return fail(DB_ERR_INVALID, "%s: fp16 weights take no scale vector", fn);
   } else if (w_dtype == DB_DTYPE_FP8_E4M3) {
-    return fail(DB_ERR_UNSUPPORTED, "%s: fp8 e4m3 weights are not implemented yet", fn);
+    if (K % 16 != 0)
+      return fail(DB_ERR_INVALID, "%s: K=%d must be a multiple of 16 for fp8 weights", fn, K);
+    if (!scale || (pair && !scale2))
+      return fail(DB_ERR_INVALID, "%s: fp8 weights need a per-row fp32 scale vector", fn);
+    if (!aligned4(scale) || (scale2 && !aligned4(scale2)))
+      return fail(DB_ERR_INVALID, "%s: scale vectors must be 4-byte aligned", fn);
   } else {
     return fail(DB_ERR_INVALID, "%s: unknown weight dtype %d", fn, w_dtype);
   }
   return DB_OK;
+}
+
+int check_norm(const char* fn, const void* g, float eps) {
+  if (!g) return fail(DB_ERR_INVALID, "%s: null gain pointer", fn);
+  if (!aligned16(g)) return fail(DB_ERR_INVALID, "%s: tensors must be 16-byte aligned", fn);
+  if (!(eps >= 0.0f) || !isfinite(eps))
+    return fail(DB_ERR_INVALID, "%s: eps must be finite and >= 0", fn);
+  return DB_OK;
+}
+
+dbk::GemvWeights weights(int w_dtype, const void* w0, const void* w1, const float* s0,
+                         const float* s1) {
+  return dbk::GemvWeights{w0, w1, s0, s1, w_dtype == DB_DTYPE_FP8_E4M3};
+}
+
+int run_gemv(const char* fn, dbk::GemvMode mode, const void* x, const void* g,
+             const dbk::GemvWeights& w, void* y, int B, int K, int N, float eps,
+             void* stream) {
+  int err = 0;
+  const int cus = dbk::device_cu_count(&err);
+  if (err) return hip_status((hipError_t)err, fn);
+  return hip_status(dbk::launch_gemv(mode, x, g, w, y, B, K, N, eps, cus, (hipStream_t)stream),
+                    fn);
 }
 
 }  // namespace
@@ -123,46 +156,42 @@ int db_f1_rmsnorm_gemv(const void* x, const void* g, const void* W,
                        const float* w_scale, void* y, int B, int K, int N,
                        float eps, int w_dtype, void* stream) {
   const char* fn = "db_f1_rmsnorm_gemv";
-  if (!g) return fail(DB_ERR_INVALID, "%s: null gain pointer", fn);
-  if (!aligned16(g)) return fail(DB_ERR_INVALID, "%s: tensors must be 16-byte aligned", fn);
-  if (!(eps >= 0.0f) || !isfinite(eps))
-    return fail(DB_ERR_INVALID, "%s: eps must be finite and >= 0", fn);
-  int rc = check_gemv(fn, x, W, y, B, K, N, w_dtype, w_scale, nullptr, nullptr);
+  int rc = check_norm(fn, g, eps);
+  if (!rc) rc = check_gemv(fn, x, W, y, B, K, N, w_dtype, w_scale, nullptr, nullptr, false);
   if (rc) return rc;
-  int err = 0;
-  const int cus = dbk::device_cu_count(&err);
-  if (err) return hip_status((hipError_t)err, fn);
-  return hip_status(dbk::launch_gemv(dbk::kGemvRmsNorm, x, g, W, nullptr, y, B, K,
-                                     N, eps, cus, (hipStream_t)stream),
-                    fn);
+  return run_gemv(fn, dbk::kGemvRmsNorm, x, g, weights(w_dtype, W, nullptr, w_scale, nullptr),
+                  y, B, K, N, eps, stream);
 }
 
 int db_f2_gateup_swiglu(const void* x, const void* Wg, const void* Wu,
                         const float* sg, const float* su, void* y, int B,
                         int K, int N, int w_dtype, void* stream) {
   const char* fn = "db_f2_gateup_swiglu";
-  if (!Wu) return fail(DB_ERR_INVALID, "%s: null tensor pointer", fn);
-  int rc = check_gemv(fn, x, Wg, y, B, K, N, w_dtype, sg, Wu, su);
+  int rc = check_gemv(fn, x, Wg, y, B, K, N, w_dtype, sg, Wu, su, true);
   if (rc) return rc;
-  int err = 0;
-  const int cus = dbk::device_cu_count(&err);
-  if (err) return hip_status((hipError_t)err, fn);
-  return hip_status(dbk::launch_gemv(dbk::kGemvSwiGLU, x, nullptr, Wg, Wu, y, B,
-                                     K, N, 0.0f, cus, (hipStream_t)stream),
-                    fn);
+  return run_gemv(fn, dbk::kGemvSwiGLU, x, nullptr, weights(w_dtype, Wg, Wu, sg, su), y, B,
+                  K, N, 0.0f, stream);
+}
+
+int db_f2_rmsnorm_gateup_swiglu(const void* x, const void* g, const void* Wg,
+                                const void* Wu, const float* sg, const float* su,
+                                void* y, int B, int K, int N, float eps,
+                                int w_dtype, void* stream) {
+  const char* fn = "db_f2_rmsnorm_gateup_swiglu";
+  int rc = check_norm(fn, g, eps);
+  if (!rc) rc = check_gemv(fn, x, Wg, y, B, K, N, w_dtype, sg, Wu, su, true);
+  if (rc) return rc;
+  return run_gemv(fn, dbk::kGemvRmsNormSwiGLU, x, g, weights(w_dtype, Wg, Wu, sg, su), y, B,
+                  K, N, eps, stream);
 }
 
 int db_gemv(const void* x, const void* W, const float* w_scale, void* y, int B,
             int K, int N, int w_dtype, void* stream) {
   const char* fn = "db_gemv";
-  int rc = check_gemv(fn, x, W, y, B, K, N, w_dtype, w_scale, nullptr, nullptr);
+  int rc = check_gemv(fn, x, W, y, B, K, N, w_dtype, w_scale, nullptr, nullptr, false);
   if (rc) return rc;
-  int err = 0;
-  const int cus = dbk::device_cu_count(&err);
-  if (err) return hip_status((hipError_t)err, fn);
-  return hip_status(dbk::launch_gemv(dbk::kGemvPlain, x, nullptr, W, nullptr, y, B,
-                                     K, N, 0.0f, cus, (hipStream_t)stream),
-                    fn);
+  return run_gemv(fn, dbk::kGemvPlain, x, nullptr, weights(w_dtype, W, nullptr, w_scale, nullptr),
+                  y, B, K, N, 0.0f, stream);
 }
 
 int db_f4_default_splits(int B, int Hkv, int L, int cu_count) {

@@ -28,6 +28,20 @@ __device__ __forceinline__ u4 ld16(const void* p) {
   return *reinterpret_cast<const u4*>(p);
 }
 
+// Raw buffer resource over `bytes` bytes at `base` (stride 0).  A buffer load
+// at an offset >= bytes returns zero without a memory access, so a kernel can
+// issue the loads of a tile that does not exist (bytes = 0) unconditionally
+// and keep one straight-line path through its load/compute pipeline.
+// Word 3 is the gfx9 data-format default for raw byte buffers.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes,
+                                           0x00020000);
+}
+// 16-byte non-temporal buffer load (cache policy bit 1 = nt).
+__device__ __forceinline__ u4 ld_buf_stream(__amdgpu_buffer_rsrc_t r, int offset) {
+  return __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 2));
+}
+
 __device__ __forceinline__ h2 as_h2(unsigned v) {
   return __builtin_bit_cast(h2, v);
 }

@@ -20,17 +20,43 @@ Tuning& tuning();
 // Compute units of the current device (cached per device ordinal).
 int device_cu_count(int* err);
 
-enum GemvMode : int { kGemvPlain = 0, kGemvRmsNorm = 1, kGemvSwiGLU = 2 };
+enum GemvMode : int {
+  kGemvPlain = 0,
+  kGemvRmsNorm = 1,
+  kGemvSwiGLU = 2,
+  kGemvRmsNormSwiGLU = 3,
+};
 
-// y[B,N] = op(x[B,K]) . W^T  (fp16 in/out, fp32 accumulation).
-//   kGemvPlain   : y = x W^T
-//   kGemvRmsNorm : y = fp16(fp16(x * rsqrt(mean(x^2) + eps)) * gamma) W^T
-//   kGemvSwiGLU  : y = fp16(silu(fp16(x Wg^T)) * fp16(x Wu^T))
+constexpr bool gemv_has_norm(int mode) {
+  return mode == kGemvRmsNorm || mode == kGemvRmsNormSwiGLU;
+}
+constexpr bool gemv_is_swiglu(int mode) {
+  return mode == kGemvSwiGLU || mode == kGemvRmsNormSwiGLU;
+}
+
+// Weights of one GEMV call: one matrix (two for the SwiGLU modes), fp16 or
+// OCP e4m3 with one fp32 scale per output row.
+struct GemvWeights {
+  const void* w0;     // [N, K]  (gate in the SwiGLU modes)
+  const void* w1;     // [N, K]  (up, SwiGLU modes only)
+  const float* s0;    // [N]     row scales of w0 (fp8 only)
+  const float* s1;    // [N]     row scales of w1 (fp8 SwiGLU only)
+  bool fp8;
+};
+
+// y[B,N] = op(x[B,K]) . W^T  (fp16 activations in/out, fp32 accumulation).
+//   kGemvPlain          : y = x W^T
+//   kGemvRmsNorm        : y = fp16(fp16(x * rsqrt(mean(x^2) + eps)) * gamma) W^T
+//   kGemvSwiGLU         : y = fp16(silu(fp16(x Wg^T)) * fp16(x Wu^T))
+//   kGemvRmsNormSwiGLU  : the SwiGLU mode on the RMS-normalised x
+// With fp8 weights every projection is fp32(sum) * row scale before its
+// fp16 rounding.
 hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
-                       const void* w0, const void* w1, void* y, int B, int K,
-                       int N, float eps, int cu_count, hipStream_t stream);
+                       const GemvWeights& w, void* y, int B, int K, int N, float eps,
+                       int cu_count, hipStream_t stream);
 
-// MFMA variant for batches of 2..16 rows per pass (gemv_mfma.hip).
+// MFMA variant for batches of 2..16 rows per pass (gemv_mfma.hip), fp16
+// weights only.
 bool gemv_mfma_supported(int B, int K, int N);
 hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
                             const void* w0, const void* w1, void* y, int B, int K,

@@ -1,9 +1,9 @@
 // gemv_mfma.hip -- batched decode GEMV on MFMA (batch 2..16 per pass) for gfx950.
 //
-// y[B,N] = op(x[B,K]) . W^T for the three GEMV modes of gemv.hip (plain,
-// RMSNorm-fused F1, gate/up + SwiGLU F2) when the batch is large enough that
-// the VALU dot-product path becomes instruction-bound (at batch 8 it runs at
-// a third of HBM speed).  The weights are still read exactly once; MFMA does
+// y[B,N] = op(x[B,K]) . W^T for the four GEMV modes of gemv.hip (plain,
+// RMSNorm-fused F1, gate/up + SwiGLU F2, RMSNorm -> gate/up + SwiGLU) with
+// fp16 weights when the batch is large enough that the VALU dot-product path
+// becomes instruction-bound (at batch 8 it runs at a third of HBM speed).  The weights are still read exactly once; MFMA does
 // the multiply-adds.
 //
 // Decomposition
@@ -29,13 +29,12 @@
 //    the last group the workgroup reduces the 8 K-slices and applies the
 //    epilogue (fp16 rounding, or SiLU(g) * u with the reference's rounding
 //    points), storing only the final fp16 outputs.
-//  * F1: each wave sums x^2 over its slice, the 8 partial sums meet in LDS,
+//  * Norm modes: each wave sums x^2 over its slice, the 8 partial sums meet in LDS,
 //    and every wave normalises its own x registers exactly as the torch stage
 //    rounds: fp16(fp16(x * inv_rms) * gamma), gamma read from an LDS copy.
 // Batches above 16 run as passes of 16 (grid.y); each pass re-reads the
 // weights.
-#include "db_device.h"
-#include "db_kernels.h"
+#include "gemv_valu.h"
 
 namespace dbk {
 
@@ -59,8 +58,6 @@ struct MfmaArgs {
   float eps;
 };
 
-__device__ __forceinline__ float silu_m(float g) { return g / (1.0f + __expf(-g)); }
-
 // KH: k-steps (32 columns each) per half slice, K / 512.
 // BT: batch column tiles of 8 (1 for batch <= 8, 2 for <= 16).
 // UPS: groups per register set.  When a workgroup's groups fit in one set
@@ -68,11 +65,11 @@ __device__ __forceinline__ float silu_m(float g) { return g / (1.0f + __expf(-g)
 // and no loop runs; otherwise two sets alternate.
 template <int MODE, int KH, int BT, int UPS, bool SINGLE>
 __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
-  constexpr int NWM = (MODE == kGemvSwiGLU) ? 2 : 1;
+  constexpr int NWM = gemv_is_swiglu(MODE) ? 2 : 1;
   // [group][matrix][wave][batch][row]
   __shared__ __align__(16) float part[kMaxGroupsPerWg][NWM][kWavesM][kBatchTile][kRowsPerGroup];
   __shared__ float red[kWavesM][kBatchTile];
-  __shared__ u4 s_gamma[MODE == kGemvRmsNorm ? kThreadsM : 1];  // K / 8 chunks
+  __shared__ u4 s_gamma[gemv_has_norm(MODE) ? kThreadsM : 1];  // K / 8 chunks
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -98,7 +95,7 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
     for (int t = 0; t < KH; ++t) xr[bt][t] = ld16(a.x + (size_t)xrow * a.K + kcol + 32 * t);
   }
   u4 gchunk = {0, 0, 0, 0};
-  if constexpr (MODE == kGemvRmsNorm)
+  if constexpr (gemv_has_norm(MODE))
     gchunk = ld16(a.gamma + 8 * min((int)threadIdx.x, a.K / 8 - 1));
   __builtin_amdgcn_sched_barrier(0);
 
@@ -134,7 +131,7 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
     for (int t = 0; t < KH; ++t) xr[bt][t] = valid ? xr[bt][t] : zero4;
   }
 
-  if constexpr (MODE == kGemvRmsNorm) {
+  if constexpr (gemv_has_norm(MODE)) {
     // x^2 over this slice per batch row: in-lane, then over the two halves
     // (lanes 8 apart) and the 4 k-groups (lanes 16 apart).
     float ss[BT];
@@ -245,10 +242,10 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
       if constexpr (NWM == 2) s1 += part[jj][NWM - 1][v][n][r];
     }
     float out;
-    if constexpr (MODE == kGemvSwiGLU) {
+    if constexpr (NWM == 2) {
       const float gq = (float)to_h(s0);
       const float uq = (float)to_h(s1);
-      out = (float)to_h(silu_m(gq)) * uq;
+      out = (float)to_h(gemv_silu(gq)) * uq;
     } else {
       out = s0;
     }
@@ -262,7 +259,12 @@ using MfmaFn = void (*)(MfmaArgs);
 // ups < 0: alternating sets of -ups groups.
 template <int MODE, int KH, int BT>
 MfmaFn pick_ups(int ups) {
-  if constexpr (MODE == kGemvSwiGLU) {
+  if constexpr (MODE == kGemvRmsNormSwiGLU && BT == 2) {
+    // The normalisation next to two batch tiles and a gate/up pair: one
+    // group pair per alternating set.
+    (void)ups;
+    return gemv_mfma_kernel<MODE, KH, BT, 1, false>;
+  } else if constexpr (gemv_is_swiglu(MODE)) {
     return ups == 2 ? gemv_mfma_kernel<MODE, KH, BT, 2, true>
                     : gemv_mfma_kernel<MODE, KH, BT, 1, false>;
   } else if constexpr (MODE == kGemvRmsNorm && BT == 2) {
@@ -294,7 +296,7 @@ MfmaFn pick_kh(int kh, int bt, int ups) {
 // matrix, 2 of the gate/up pair, at 8 or 16 loads per group and matrix),
 // else alternating sets of 2 groups (1 for the pair).  See pick_ups.
 int pick_sets(GemvMode mode, int gpw) {
-  if (mode == kGemvSwiGLU) return gpw <= 2 ? 2 : -1;
+  if (gemv_is_swiglu(mode)) return gpw <= 2 ? 2 : -1;
   return gpw <= 2 ? 2 : (gpw <= 4 ? gpw : -2);
 }
 
@@ -333,6 +335,7 @@ hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
   switch (mode) {
     case kGemvRmsNorm: fn = pick_kh<kGemvRmsNorm>(kh, bt, ups); break;
     case kGemvSwiGLU: fn = pick_kh<kGemvSwiGLU>(kh, bt, ups); break;
+    case kGemvRmsNormSwiGLU: fn = pick_kh<kGemvRmsNormSwiGLU>(kh, bt, ups); break;
     default: fn = pick_kh<kGemvPlain>(kh, bt, ups); break;
   }
   dim3 g(grid, (B + kBatchTile - 1) / kBatchTile);

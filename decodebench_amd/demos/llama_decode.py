@@ -11,7 +11,10 @@ Two builders:
 * ``build_config(name, batch=1, ...)`` builds the MI355X benchmark
   configurations: F1 ``W[4096,4096]`` (config 1), F1-QKV ``W[6144,4096]``
   (config 3), F2 ``[14336,4096]`` (config 2), F4 with 32 query / 8 KV heads
-  and scale 1/sqrt(128) (config 4).  It returns a :class:`Case` that also
+  and scale 1/sqrt(128) (config 4), and the Llama-3-8B-shaped decode layer
+  (config 5: RMSNorm -> QKV -> attention -> O -> RMSNorm -> gate/up SwiGLU ->
+  down).  ``dtype="fp8"`` stores the projection weights as OCP e4m3 with
+  one fp32 scale per output row.  It returns a :class:`Case` that also
   carries the fused HIP callable, the algorithmic bytes and a replica list
   sized to defeat the whole cache hierarchy (8 L2s + the 256 MB MALL).
 
@@ -34,7 +37,8 @@ from decodebench_amd.sequence import Sequence
 from decodebench_amd.timing import cache_defeat_replicas, n_weight_replicas
 
 DEMO_NAMES = ("f1", "f2", "f4")
-CONFIG_NAMES = ("f1", "f1_qkv", "f2", "f4")
+CONFIG_NAMES = ("f1", "f1_qkv", "f2", "f4", "layer")
+DTYPES = ("f16", "fp8")
 _FFN = {2048: 8192, 4096: 11008}
 _L = 1024
 _HEAD_DIM = 128
@@ -123,6 +127,177 @@ def f4_sequence(scale: float = 1.0) -> Sequence:
     return seq
 
 
+def _linear_fp8(a, W, s):
+    """The fp8 projection stage: e4m3 weights dequantised exactly, fp32
+    accumulation, the row scale applied before the fp16 rounding."""
+    import torch
+
+    return (torch.nn.functional.linear(a.float(), W.float()) * s).half()
+
+
+def f1_fp8_sequence(eps: float = 1e-6) -> Sequence:
+    import torch
+
+    seq = Sequence("f1_fp8")
+
+    @seq.stage
+    def rmsnorm(x, g):
+        var = x.float().pow(2).mean(dim=-1, keepdim=True)
+        return (x.float() * torch.rsqrt(var + eps)).half() * g
+
+    @seq.stage
+    def gemv(xh, W, s):
+        return _linear_fp8(xh, W, s)
+
+    return seq
+
+
+def f2_fp8_sequence() -> Sequence:
+    import torch
+
+    seq = Sequence("f2_fp8")
+
+    @seq.stage
+    def gate(xh, Wg, sg):
+        return _linear_fp8(xh, Wg, sg)
+
+    @seq.stage
+    def up(xh, Wu, su):
+        return _linear_fp8(xh, Wu, su)
+
+    @seq.stage
+    def swiglu(up, gate):
+        return torch.nn.functional.silu(gate) * up
+
+    return seq
+
+
+def layer_sequence(n_q_heads: int, scale: float, eps: float = 1e-6,
+                   fp8: bool = False) -> Sequence:
+    """The decode-layer chain as single-op torch stages: rmsnorm, QKV, the
+    query heads of QKV (copied: a stage returns a tensor of its own), scores,
+    softmax, weighted V, O projection, rmsnorm, gate, up, SwiGLU, down.
+
+    The new token's k and v columns of QKV are not appended to the cache:
+    the chain measures the decode read path over a given KV cache."""
+    import torch
+
+    F = torch.nn.functional
+    seq = Sequence("layer_fp8" if fp8 else "layer")
+
+    def norm(x, g):
+        var = x.float().pow(2).mean(dim=-1, keepdim=True)
+        return (x.float() * torch.rsqrt(var + eps)).half() * g
+
+    @seq.stage
+    def rmsnorm1(x, g1):
+        return norm(x, g1)
+
+    if fp8:
+        @seq.stage
+        def qkv(rmsnorm1, Wqkv, s_qkv):
+            return _linear_fp8(rmsnorm1, Wqkv, s_qkv)
+    else:
+        @seq.stage
+        def qkv(rmsnorm1, Wqkv):
+            return F.linear(rmsnorm1, Wqkv)
+
+    @seq.stage
+    def q_heads(qkv):
+        B = qkv.shape[0]
+        return qkv[:, : n_q_heads * _HEAD_DIM].reshape(B, n_q_heads, _HEAD_DIM).clone()
+
+    @seq.stage
+    def scores(q_heads, K):
+        B, Hq, D = q_heads.shape
+        Hkv = K.shape[1]
+        qt = q_heads.reshape(B, Hkv, Hq // Hkv, D).transpose(-1, -2).contiguous()
+        s = torch.matmul(K, qt)
+        return s.transpose(-1, -2).float().mul(scale).reshape(B, Hq, K.shape[2])
+
+    @seq.stage
+    def softmax(scores):
+        return torch.softmax(scores, dim=-1)
+
+    @seq.stage
+    def weighted_v(softmax, V):
+        B, Hq, L = softmax.shape
+        Hkv = V.shape[1]
+        pg = softmax.half().reshape(B, Hkv, Hq // Hkv, L)
+        return torch.matmul(pg, V).reshape(B, Hq * V.shape[3])
+
+    if fp8:
+        @seq.stage
+        def o_proj(weighted_v, Wo, s_o):
+            return _linear_fp8(weighted_v, Wo, s_o)
+    else:
+        @seq.stage
+        def o_proj(weighted_v, Wo):
+            return F.linear(weighted_v, Wo)
+
+    @seq.stage
+    def rmsnorm2(o_proj, g2):
+        return norm(o_proj, g2)
+
+    if fp8:
+        @seq.stage
+        def gate(rmsnorm2, Wg, s_gate):
+            return _linear_fp8(rmsnorm2, Wg, s_gate)
+
+        @seq.stage
+        def up(rmsnorm2, Wu, s_up):
+            return _linear_fp8(rmsnorm2, Wu, s_up)
+    else:
+        @seq.stage
+        def gate(rmsnorm2, Wg):
+            return F.linear(rmsnorm2, Wg)
+
+        @seq.stage
+        def up(rmsnorm2, Wu):
+            return F.linear(rmsnorm2, Wu)
+
+    @seq.stage
+    def swiglu(up, gate):
+        return F.silu(gate) * up
+
+    if fp8:
+        @seq.stage
+        def down(swiglu, Wd, s_down):
+            return _linear_fp8(swiglu, Wd, s_down)
+    else:
+        @seq.stage
+        def down(swiglu, Wd):
+            return F.linear(swiglu, Wd)
+
+    return seq
+
+
+def layer_fused(n_q_heads: int, scale: float, eps: float = 1e-6,
+                n_splits: int | None = None) -> Callable[[dict], object]:
+    """The decode layer on the HIP kernels: F1 (RMSNorm -> QKV), F4 (two
+    launches), the O projection, RMSNorm -> gate/up SwiGLU in one kernel, and
+    the down projection.  fp16 or e4m3 weights, as the inputs hold them."""
+    from decodebench_amd import ops
+
+    def run(inp):
+        import torch
+
+        fp8 = inp["Wqkv"].dtype != torch.float16
+        sc = (lambda k: inp[k]) if fp8 else (lambda k: None)
+        x = inp["x"]
+        B = x.shape[0]
+        qkv = ops.f1_rmsnorm_gemv(x, inp["g1"], inp["Wqkv"], eps, w_scale=sc("s_qkv"))
+        q = qkv[:, : n_q_heads * _HEAD_DIM]
+        q = (q if B == 1 else q.contiguous()).view(B, n_q_heads, _HEAD_DIM)
+        attn = ops.f4_flashdecode(q, inp["K"], inp["V"], scale=scale, n_splits=n_splits)
+        h = ops.gemv(attn.view(B, n_q_heads * _HEAD_DIM), inp["Wo"], w_scale=sc("s_o"))
+        ff = ops.f2_rmsnorm_gateup_swiglu(h, inp["g2"], inp["Wg"], inp["Wu"], eps,
+                                          sg=sc("s_gate"), su=sc("s_up"))
+        return ops.gemv(ff, inp["Wd"], w_scale=sc("s_down"))
+
+    return run
+
+
 # --------------------------------------------------- reference-shaped demos
 def _build_f1(dim: int, batch: int, seed: int):
     import torch
@@ -208,17 +383,41 @@ def _replicate(inputs: dict, big: tuple[str, ...], n: int) -> list[dict]:
     return reps
 
 
+# Llama-3-8B layer shape of the decode chain.
+LAYER = {"d": 4096, "Hq": 32, "Hkv": 8, "D": _HEAD_DIM, "F": 14336}
+
+
+def _weight(gen, shape, std, device, fp8: bool):
+    """An fp16 weight matrix, or its e4m3 quantisation and row scales."""
+    W = _randn(gen, shape, std=std, device=device)
+    if not fp8:
+        return W, None
+    from decodebench_amd.quant import quantize_e4m3_rows
+
+    return quantize_e4m3_rows(W)
+
+
 def build_config(name: str, batch: int = 1, L: int = 8192, n_splits: int | None = None,
                  seed: int = 42, device="cuda", replicas: int | None = None,
-                 K: int = 4096, gen_device: str = "cpu") -> Case:
+                 K: int = 4096, gen_device: str = "cpu", dtype: str = "f16") -> Case:
     """BASELINE-shaped case; ``replicas=None`` sizes a cache-defeating rotation.
 
     ``gen_device="cpu"`` draws the inputs on the CPU (device-independent
-    values, what the parity tests use); ``"cuda"`` draws them on the GPU."""
+    values, what the parity tests use); ``"cuda"`` draws them on the GPU.
+    ``dtype="fp8"`` (F1, F1-QKV, F2 and the layer) quantises the projection
+    weights to e4m3 with per-row scales; algorithmic bytes then count one
+    byte per weight plus four per row scale."""
     import torch
 
     from decodebench_amd import ops
 
+    if dtype not in DTYPES:
+        raise ValueError(f"unknown dtype '{dtype}'; choose from {list(DTYPES)}")
+    fp8 = dtype == "fp8"
+    if fp8 and name == "f4":
+        raise ValueError("f4 has no weights; dtype='fp8' applies to f1, f1_qkv, f2, layer")
+    wb = 1 if fp8 else 2            # bytes per weight
+    sb = 4 if fp8 else 0            # bytes of row scale per output row
     gen = torch.Generator(device=gen_device).manual_seed(seed)
     B = batch
     if name in ("f1", "f1_qkv"):
@@ -226,26 +425,66 @@ def build_config(name: str, batch: int = 1, L: int = 8192, n_splits: int | None 
         w_std = 1.0 / 64.0 if name == "f1" else 0.02
         x = _randn(gen, (B, K), device=device)
         g = _randn(gen, (K,), std=0.1, mean=1.0, device=device)
-        W = _randn(gen, (N, K), std=w_std, device=device)
-        inputs = {"x": x, "g": g, "W": W}
-        seq = f1_sequence(1e-6)
-        fused = lambda inp: ops.f1_rmsnorm_gemv(inp["x"], inp["g"], inp["W"], 1e-6)  # noqa: E731
+        W, s = _weight(gen, (N, K), w_std, device, fp8)
+        if fp8:
+            inputs = {"x": x, "g": g, "W": W, "s": s}
+            seq = f1_fp8_sequence(1e-6)
+            fused = lambda inp: ops.f1_rmsnorm_gemv(inp["x"], inp["g"], inp["W"], 1e-6,  # noqa: E731
+                                                    w_scale=inp["s"])
+        else:
+            inputs = {"x": x, "g": g, "W": W}
+            seq = f1_sequence(1e-6)
+            fused = lambda inp: ops.f1_rmsnorm_gemv(inp["x"], inp["g"], inp["W"], 1e-6)  # noqa: E731
         big = ("W",)
-        nbytes = N * K * 2 + K * 2 + B * (K + N) * 2
+        nbytes = N * K * wb + N * sb + K * 2 + B * (K + N) * 2
         flops = 2 * B * N * K
-        shape = {"B": B, "K": K, "N": N}
+        shape = {"B": B, "K": K, "N": N, "dtype": dtype}
     elif name == "f2":
         N = 14336
         x = _randn(gen, (B, K), device=device)
-        Wg = _randn(gen, (N, K), std=0.02, device=device)
-        Wu = _randn(gen, (N, K), std=0.02, device=device)
-        inputs = {"xh": x, "Wg": Wg, "Wu": Wu}
-        seq = f2_sequence()
-        fused = lambda inp: ops.f2_gateup_swiglu(inp["xh"], inp["Wg"], inp["Wu"])  # noqa: E731
+        Wg, sg = _weight(gen, (N, K), 0.02, device, fp8)
+        Wu, su = _weight(gen, (N, K), 0.02, device, fp8)
+        if fp8:
+            inputs = {"xh": x, "Wg": Wg, "Wu": Wu, "sg": sg, "su": su}
+            seq = f2_fp8_sequence()
+            fused = lambda inp: ops.f2_gateup_swiglu(inp["xh"], inp["Wg"], inp["Wu"],  # noqa: E731
+                                                     inp["sg"], inp["su"])
+        else:
+            inputs = {"xh": x, "Wg": Wg, "Wu": Wu}
+            seq = f2_sequence()
+            fused = lambda inp: ops.f2_gateup_swiglu(inp["xh"], inp["Wg"], inp["Wu"])  # noqa: E731
         big = ("Wg", "Wu")
-        nbytes = 2 * N * K * 2 + B * (K + N) * 2
+        nbytes = 2 * N * K * wb + 2 * N * sb + B * (K + N) * 2
         flops = 4 * B * N * K
-        shape = {"B": B, "K": K, "N": N}
+        shape = {"B": B, "K": K, "N": N, "dtype": dtype}
+    elif name == "layer":
+        d, Hq, Hkv, D, F = (LAYER[k] for k in ("d", "Hq", "Hkv", "D", "F"))
+        Nqkv = (Hq + 2 * Hkv) * D
+        x = _randn(gen, (B, d), device=device)
+        g1 = _randn(gen, (d,), std=0.1, mean=1.0, device=device)
+        g2 = _randn(gen, (d,), std=0.1, mean=1.0, device=device)
+        Wqkv, s_qkv = _weight(gen, (Nqkv, d), 0.02, device, fp8)
+        Kc = _randn(gen, (B, Hkv, L, D), device=device)
+        Vc = _randn(gen, (B, Hkv, L, D), device=device)
+        Wo, s_o = _weight(gen, (d, Hq * D), 0.02, device, fp8)
+        Wg, s_gate = _weight(gen, (F, d), 0.02, device, fp8)
+        Wu, s_up = _weight(gen, (F, d), 0.02, device, fp8)
+        Wd, s_down = _weight(gen, (d, F), 0.02, device, fp8)
+        inputs = {"x": x, "g1": g1, "Wqkv": Wqkv, "K": Kc, "V": Vc, "Wo": Wo, "g2": g2,
+                  "Wg": Wg, "Wu": Wu, "Wd": Wd, "s_qkv": s_qkv, "s_o": s_o,
+                  "s_gate": s_gate, "s_up": s_up, "s_down": s_down}
+        if not fp8:  # the fp16 stages take no scales
+            inputs = {k: v for k, v in inputs.items() if not k.startswith("s_")}
+        scale = 1.0 / math.sqrt(D)
+        seq = layer_sequence(Hq, scale, 1e-6, fp8)
+        fused = layer_fused(Hq, scale, 1e-6, n_splits)
+        big = ("Wqkv", "K", "V", "Wo", "Wg", "Wu", "Wd")
+        rows = Nqkv + d + 2 * F + d
+        wbytes = (Nqkv * d + d * Hq * D + 2 * F * d + d * F) * wb + rows * sb
+        nbytes = wbytes + 2 * B * Hkv * L * D * 2 + 2 * d * 2 + 2 * B * d * 2
+        flops = 2 * B * (Nqkv * d + d * Hq * D + 2 * F * d + d * F) + 4 * B * Hq * L * D
+        shape = {"B": B, "d": d, "Hq": Hq, "Hkv": Hkv, "L": L, "D": D, "F": F,
+                 "S": n_splits, "dtype": dtype}
     elif name == "f4":
         Hq, Hkv, D = 32, 8, _HEAD_DIM
         q = _randn(gen, (B, Hq, D), device=device)

@@ -60,6 +60,8 @@ def load_library():
             "db_device_cu_count": (_i, [C.POINTER(_i)]),
             "db_f1_rmsnorm_gemv": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, C.c_float, _i, _p]),
             "db_f2_gateup_swiglu": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p]),
+            "db_f2_rmsnorm_gateup_swiglu": (_i, [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i,
+                                                 C.c_float, _i, _p]),
             "db_gemv": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p]),
             "db_f4_default_splits": (_i, [_i, _i, _i, _i]),
             "db_f4_workspace_bytes": (C.c_size_t, [_i, _i, _i, _i, _i, _i]),
@@ -195,6 +197,36 @@ def f2_gateup_swiglu(x, Wg, Wu, sg=None, su=None):
                                             sgp, sup, y.data_ptr(), B, K, N, dt,
                                             _stream_ptr(x))
     _check(rc, "db_f2_gateup_swiglu")
+    return y[0] if squeeze else y
+
+
+def f2_rmsnorm_gateup_swiglu(x, g, Wg, Wu, eps: float = 1e-6, sg=None, su=None):
+    """RMSNorm -> F2 in one kernel: ``f2_gateup_swiglu(rmsnorm(x, g, eps), Wg, Wu)``
+    with the normalised activations kept on chip (the post-attention half
+    of the decode-layer chain).
+
+    x [B,K] (or [K]) fp16, g [K] fp16, Wg/Wu [N,K] fp16 (or e4m3 + per-row
+    scales).  Returns [B,N] fp16 (or [N])."""
+    import torch
+
+    _require(x, "x", torch.float16)
+    _require(g, "g", torch.float16)
+    _require(Wg, "Wg")
+    _require(Wu, "Wu")
+    x2, squeeze = _as_2d(x, "x")
+    B, K = x2.shape
+    if (Wg.dim() != 2 or Wg.shape != Wu.shape or Wg.shape[1] != K or Wg.dtype != Wu.dtype
+            or g.shape != (K,)):
+        raise ValueError(f"shape mismatch: x {tuple(x.shape)}, g {tuple(g.shape)}, "
+                         f"Wg {tuple(Wg.shape)}, Wu {tuple(Wu.shape)}")
+    N = Wg.shape[0]
+    dt, sgp = _weights(Wg, sg, "Wg", N, K)
+    _, sup = _weights(Wu, su, "Wu", N, K)
+    y = torch.empty((B, N), dtype=torch.float16, device=x.device)
+    rc = load_library().db_f2_rmsnorm_gateup_swiglu(
+        x2.data_ptr(), g.data_ptr(), Wg.data_ptr(), Wu.data_ptr(), sgp, sup, y.data_ptr(),
+        B, K, N, float(eps), dt, _stream_ptr(x))
+    _check(rc, "db_f2_rmsnorm_gateup_swiglu")
     return y[0] if squeeze else y
 
 

@@ -65,7 +65,9 @@ int db_device_cu_count(int* cu_count);
  * (src/decodebench/demos/llama_decode.py:36-43).
  * Contract: B >= 1, N >= 1, K >= 8 and K % 8 == 0; x [B,K], g [K], W [N,K],
  * y [B,N] fp16.  w_dtype must be DB_DTYPE_F16 (w_scale NULL) or
- * DB_DTYPE_FP8_E4M3 (w_scale [N] fp32, W holds N*K bytes). */
+ * DB_DTYPE_FP8_E4M3: W then holds N*K OCP e4m3fn bytes, K % 16 == 0, and
+ * w_scale [N] fp32 (4-byte aligned) multiplies each row's fp32 dot product
+ * before its fp16 rounding: y = fp16(w_scale[n] * sum_k e4m3(W[n,k]) xh[k]). */
 int db_f1_rmsnorm_gemv(const void* x, const void* g, const void* W,
                        const float* w_scale, void* y, int B, int K, int N,
                        float eps, int w_dtype, void* stream);
@@ -80,6 +82,21 @@ int db_f1_rmsnorm_gemv(const void* x, const void* g, const void* W,
 int db_f2_gateup_swiglu(const void* x, const void* Wg, const void* Wu,
                         const float* sg, const float* su, void* y, int B,
                         int K, int N, int w_dtype, void* stream);
+
+/* RMSNorm -> F2 in one kernel: y = F2(xh) with xh the F1 normalisation of x
+ * (fp32 statistic, fp16(fp16(x * inv_rms) * g)), built once per workgroup in
+ * LDS, so neither the normalised vector nor the gate/up projections reach
+ * HBM.  It is the post-attention half of the decode-layer chain (rmsnorm
+ * followed by gate, up, swiglu, src/decodebench/demos/llama_decode.py:36-39,
+ * 77-87); the reference has no single fused kernel for the pair, so this
+ * replaces the f1 prologue of f1_kernel (validation/src/kernels/fused/
+ * f1.cu:18-50) feeding f2_kernel (f2.cu:17-76).
+ * Contract as db_f2_gateup_swiglu, plus g [K] fp16 and eps as in
+ * db_f1_rmsnorm_gemv. */
+int db_f2_rmsnorm_gateup_swiglu(const void* x, const void* g, const void* Wg,
+                                const void* Wu, const float* sg, const float* su,
+                                void* y, int B, int K, int N, float eps,
+                                int w_dtype, void* stream);
 
 /* Plain GEMV y[B,N] = fp16( x[B,K] . W[N,K]^T ) with fp32 accumulation: the
  * unfused projection of the decode-layer chain (O and down projections).

@@ -212,3 +212,15 @@ def gemv_fp8_exact(x, Wq, scale) -> np.ndarray:
     load().orc_gemv_fp8_f64(_h(x), np.ascontiguousarray(Wq, dtype=np.uint8),
                             np.ascontiguousarray(scale, dtype=np.float32), out, B, K, N)
     return out
+
+
+def f1_fp8_exact(x, g, Wq, scale, eps: float = 1e-6) -> np.ndarray:
+    """fp8 F1: the fp16-rounded normalised activation, then an exact fp8 GEMV."""
+    return gemv_fp8_exact(rmsnorm(x, g, eps), Wq, scale)
+
+
+def f2_fp8_exact(x, Wgq, sg, Wuq, su) -> np.ndarray:
+    """silu(g) * u of the exact fp8 gate and up projections (double)."""
+    g = gemv_fp8_exact(x, Wgq, sg)
+    u = gemv_fp8_exact(x, Wuq, su)
+    return g / (1.0 + np.exp(-g)) * u

@@ -88,18 +88,46 @@ def f4(q, K, V, scale: float | None = None) -> torch.Tensor:
     return weighted_v(softmax(scores(q, K, scale)), V)
 
 
+# ------------------------------------------------ fp8 e4m3 weight stages
+def gemv_fp8(xh: torch.Tensor, Wq: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """gemv with OCP e4m3 weights and one fp32 scale per output row:
+    fp16(scale * (xh . e4m3(Wq)^T)), dequantised exactly and accumulated in
+    fp32 (the reference has no fp8 stage; this is the definition the fp8
+    entry points follow: dequantise-then-GEMV equals GEMV-then-scale)."""
+    return (F.linear(xh.float(), Wq.float()) * scale.float()).half()
+
+
+def f1_fp8(x, g, Wq, s, eps: float = 1e-6) -> torch.Tensor:
+    return gemv_fp8(rmsnorm(x, g, eps), Wq, s)
+
+
+def f2_fp8(x, Wgq, sg, Wuq, su) -> torch.Tensor:
+    return swiglu(gemv_fp8(x, Wuq, su), gemv_fp8(x, Wgq, sg))
+
+
+def f2_rmsnorm(x, g, Wg, Wu, eps: float = 1e-6) -> torch.Tensor:
+    """rmsnorm followed by the F2 stages (the chain's post-attention half)."""
+    return f2(rmsnorm(x, g, eps), Wg, Wu)
+
+
 def decode_layer(x, g1, Wqkv, K, V, Wo, g2, Wg, Wu, Wd, n_q_heads: int,
-                 eps: float = 1e-6) -> torch.Tensor:
+                 eps: float = 1e-6, scales: dict | None = None) -> torch.Tensor:
     """Config-5 chain: RMSNorm -> QKV -> attention -> O -> RMSNorm -> SwiGLU -> down.
 
     x [B,d]; Wqkv [(Hq+2Hkv)*D, d]; K/V cache [B,Hkv,L,D] (the new token's k, v
     are not appended: the chain measures the decode read path); Wo [d, Hq*D];
-    Wg/Wu [F, d]; Wd [d, F]."""
+    Wg/Wu [F, d]; Wd [d, F].  With ``scales`` (keys "qkv", "o", "gate", "up",
+    "down") the weights are e4m3 and every projection is gemv_fp8."""
     B = x.shape[0]
-    Hkv, D = K.shape[1], K.shape[3]
-    qkv = gemv(rmsnorm(x, g1, eps), Wqkv)
+    D = K.shape[3]
+
+    def proj(a, W, key):
+        return gemv(a, W) if scales is None else gemv_fp8(a, W, scales[key])
+
+    qkv = proj(rmsnorm(x, g1, eps), Wqkv, "qkv")
     q = qkv[:, : n_q_heads * D].reshape(B, n_q_heads, D).contiguous()
     attn = f4(q, K, V).reshape(B, n_q_heads * D)
-    h = gemv(attn, Wo)
-    ff = f2(rmsnorm(h, g2, eps), Wg, Wu)
-    return gemv(ff, Wd)
+    h = proj(attn, Wo, "o")
+    hn = rmsnorm(h, g2, eps)
+    ff = swiglu(proj(hn, Wu, "up"), proj(hn, Wg, "gate"))
+    return proj(ff, Wd, "down")

@@ -35,7 +35,8 @@ def declared_functions():
 def test_header_declares_the_entry_points():
     names = declared_functions()
     for want in ("db_abi_version", "db_last_error", "db_f1_rmsnorm_gemv",
-                 "db_f2_gateup_swiglu", "db_gemv", "db_f4_splitkv",
+                 "db_f2_gateup_swiglu", "db_f2_rmsnorm_gateup_swiglu", "db_gemv",
+                 "db_f4_splitkv",
                  "db_f4_workspace_bytes", "db_f4_default_splits", "db_device_cu_count",
                  "db_tune"):
         assert want in names
@@ -79,6 +80,38 @@ def test_f2_and_gemv_contract_errors(lib):
     assert lib.db_gemv(P, P, None, P, 1, 12, 16, 0, None) == -1
 
 
+def test_f2_rmsnorm_contract_errors(lib):
+    f = lib.db_f2_rmsnorm_gateup_swiglu
+    assert f(P, None, P, P, None, None, P, 1, 4096, 14336, 1e-6, 0, None) == -1
+    assert "gain" in last(lib)
+    assert f(P, P, P, None, None, None, P, 1, 4096, 14336, 1e-6, 0, None) == -1
+    assert "null" in last(lib)
+    assert f(P, P, P, P, None, None, P, 1, 4096, 14336, float("nan"), 0, None) == -1
+    assert "eps" in last(lib)
+    assert f(P, P + 8, P, P, None, None, P, 1, 4096, 14336, 1e-6, 0, None) == -1
+    assert "aligned" in last(lib)
+
+
+def test_fp8_weight_contract_errors(lib):
+    """fp8 e4m3 weights: K % 16, a scale vector per matrix, 4-byte aligned
+    scales.  (No call here passes the contract: that would reach the GPU.)"""
+    S = C.c_void_p(P)
+    f1 = lib.db_f1_rmsnorm_gemv
+    assert f1(P, P, P, None, P, 1, 4096, 4096, 1e-6, 1, None) == -1
+    assert "scale" in last(lib)
+    assert f1(P, P, P, S, P, 1, 4104, 4096, 1e-6, 1, None) == -1
+    assert "multiple of 16" in last(lib)
+    assert f1(P, P, P, C.c_void_p(P + 2), P, 1, 4096, 4096, 1e-6, 1, None) == -1
+    assert "4-byte" in last(lib)
+    f2 = lib.db_f2_gateup_swiglu
+    assert f2(P, P, P, S, None, P, 1, 4096, 14336, 1, None) == -1
+    assert "scale" in last(lib)
+    assert lib.db_gemv(P, P, None, P, 1, 4096, 4096, 1, None) == -1
+    assert "scale" in last(lib)
+    assert lib.db_f2_rmsnorm_gateup_swiglu(P, P, P, P, S, None, P, 1, 4096, 14336, 1e-6, 1,
+                                           None) == -1
+
+
 def test_f4_contract_errors(lib):
     f = lib.db_f4_splitkv
     ok = dict(B=1, Hq=32, Hkv=8, L=1024, D=128, S=4)
@@ -114,6 +147,16 @@ def test_tune_keys(lib):
     assert lib.db_tune(b"f4_waves", 5) == -1
     assert lib.db_tune(b"f4_blocks_per_cu", 2) == 0
     assert lib.db_tune(b"f4_blocks_per_cu", 1) == 0   # back to the default
+
+
+def test_python_wrappers_check_fp8_scales():
+    torch = pytest.importorskip("torch")
+    from decodebench_amd import ops
+
+    x = torch.zeros(1, 64, dtype=torch.float16)
+    Wq = torch.zeros(8, 64, dtype=torch.float8_e4m3fn)
+    with pytest.raises(ValueError):
+        ops.gemv(x, Wq)  # CPU tensors and no scale: rejected before any launch
 
 
 def test_python_wrappers_raise_on_cpu_tensors():

@@ -25,6 +25,7 @@ from oracle import cref, stages  # noqa: E402
 pytestmark = pytest.mark.gpu
 
 RTOL = ATOL = 1e-2
+CHAIN_TOL = 2e-2     # the decode-layer chain (see test_decode_layer_chain_parity)
 F12_REL_L2 = 2e-3
 F4_REL_L2 = 5e-3
 
@@ -40,12 +41,12 @@ def randn(gen, shape, std=1.0, mean=0.0):
     return (t * std + mean).half()
 
 
-def assert_parity(got, stage_ref, exact, rel_bound, what):
+def assert_parity(got, stage_ref, exact, rel_bound, what, tol=RTOL):
     got = got.detach().float().cpu().numpy().astype(np.float64)
     ref = stage_ref.float().numpy().astype(np.float64)
     assert np.isfinite(got).all(), f"{what}: non-finite output"
-    bad = ~np.isclose(got, ref, rtol=RTOL, atol=ATOL)
-    assert not bad.any(), (f"{what}: {bad.sum()} elements outside rtol/atol 1e-2; "
+    bad = ~np.isclose(got, ref, rtol=tol, atol=tol)
+    assert not bad.any(), (f"{what}: {bad.sum()} elements outside rtol/atol {tol}; "
                            f"max abs err {np.abs(got - ref).max():.3e}")
     err = rel_l2(got, exact)
     assert err <= rel_bound, f"{what}: rel-L2 {err:.3e} > {rel_bound}"
@@ -179,6 +180,94 @@ def test_mfma_and_valu_gemv_paths_agree():
         assert rel_l2(a.float().cpu().numpy(), b.float().cpu().numpy()) < 1e-3
 
 
+# ------------------------------------------- RMSNorm -> gate/up + SwiGLU
+# One kernel for the decode chain's post-attention half; batch 1 takes the
+# VALU kernel, batches of 2..16 (and passes of 16) the MFMA kernel.
+F2N_CASES = [(1, 4096, 14336), (1, 1024, 300), (1, 4104, 64), (4, 4096, 1000),
+             (17, 4096, 600), (2, 2048, 777), (9, 512, 40)]
+
+
+@pytest.mark.parametrize("B,K,N", F2N_CASES)
+def test_f2_rmsnorm_gateup_swiglu_parity(B, K, N):
+    print(f"[f2n] B={B} K={K} N={N}", flush=True)
+    gen = torch.Generator().manual_seed(5000 + B + K + N)
+    x = randn(gen, (B, K))
+    g = randn(gen, (K,), std=0.1, mean=1.0)
+    Wg = randn(gen, (N, K), std=0.02)
+    Wu = randn(gen, (N, K), std=0.02)
+    y = ops.f2_rmsnorm_gateup_swiglu(x.cuda(), g.cuda(), Wg.cuda(), Wu.cuda(), eps=1e-6)
+    torch.cuda.synchronize()
+    assert y.shape == (B, N)
+    ref = stages.f2_rmsnorm(x, g, Wg, Wu, 1e-6)
+    xh = cref.rmsnorm(x.numpy(), g.numpy(), 1e-6)
+    exact = cref.f2_exact(xh, Wg.numpy(), Wu.numpy())
+    assert_parity(y, ref, exact, 5e-3, f"f2n B={B} K={K} N={N}")
+
+
+# ------------------------------------------------------- fp8 e4m3 weights
+# OCP e4m3 weights with per-row fp32 scales (quantize_e4m3_rows), the four
+# GEMV modes, decode-chain shapes (QKV, O, gate/up, down) plus ragged ones:
+# K not a multiple of the 1 KB row step, N not a multiple of the row group,
+# batches that take several passes.
+FP8_CASES = [
+    ("f1", 1, 4096, 6144), ("f1", 1, 4096, 4096), ("f1", 3, 4112, 131), ("f1", 9, 1024, 64),
+    ("f2", 1, 4096, 14336), ("f2", 2, 2048, 333), ("f2", 8, 4096, 1000),
+    ("f2n", 1, 4096, 14336), ("f2n", 5, 4096, 257),
+    ("plain", 1, 14336, 4096), ("plain", 1, 4096, 4096), ("plain", 4, 14336, 512),
+    ("plain", 1, 16, 5), ("plain", 12, 4096, 300),
+]
+
+
+@pytest.mark.parametrize("mode,B,K,N", FP8_CASES)
+def test_fp8_weight_gemv_parity(mode, B, K, N):
+    from decodebench_amd.quant import quantize_e4m3_rows
+
+    print(f"[fp8] {mode} B={B} K={K} N={N}", flush=True)
+    gen = torch.Generator().manual_seed(6000 + B + K + N)
+    x = randn(gen, (B, K))
+    g = randn(gen, (K,), std=0.1, mean=1.0)
+    Wq, s = quantize_e4m3_rows(randn(gen, (N, K), std=0.02))
+    W2q, s2 = quantize_e4m3_rows(randn(gen, (N, K), std=0.02))
+    bits, bits2 = Wq.view(torch.uint8).numpy(), W2q.view(torch.uint8).numpy()
+    xd, gd = x.cuda(), g.cuda()
+    if mode == "f1":
+        y = ops.f1_rmsnorm_gemv(xd, gd, Wq.cuda(), w_scale=s.cuda())
+        ref = stages.f1_fp8(x, g, Wq, s)
+        exact, bound = cref.f1_fp8_exact(x.numpy(), g.numpy(), bits, s.numpy()), F12_REL_L2
+    elif mode in ("f2", "f2n"):
+        if mode == "f2":
+            y = ops.f2_gateup_swiglu(xd, Wq.cuda(), W2q.cuda(), s.cuda(), s2.cuda())
+            xin, xin_np = x, x.numpy()
+        else:
+            y = ops.f2_rmsnorm_gateup_swiglu(xd, gd, Wq.cuda(), W2q.cuda(), sg=s.cuda(),
+                                             su=s2.cuda())
+            xin = stages.rmsnorm(x, g)
+            xin_np = cref.rmsnorm(x.numpy(), g.numpy())
+        ref = stages.f2_fp8(xin, Wq, s, W2q, s2)
+        exact, bound = cref.f2_fp8_exact(xin_np, bits, s.numpy(), bits2, s2.numpy()), 5e-3
+    else:
+        y = ops.gemv(xd, Wq.cuda(), w_scale=s.cuda())
+        ref = stages.gemv_fp8(x, Wq, s)
+        exact, bound = cref.gemv_fp8_exact(x.numpy(), bits, s.numpy()), F12_REL_L2
+    torch.cuda.synchronize()
+    assert y.shape == (B, N)
+    assert_parity(y, ref, exact, bound, f"fp8 {mode} B={B} K={K} N={N}")
+
+
+def test_fp8_raw_byte_weights_equal_float8_tensor():
+    """A uint8 view of the same e4m3 bytes is accepted and gives identical
+    results (callers may hold fp8 weights as raw bytes)."""
+    from decodebench_amd.quant import quantize_e4m3_rows
+
+    gen = torch.Generator().manual_seed(61)
+    x = randn(gen, (1, 4096)).cuda()
+    Wq, s = quantize_e4m3_rows(randn(gen, (4096, 4096), std=0.02))
+    Wq, s = Wq.cuda(), s.cuda()
+    a = ops.gemv(x, Wq, w_scale=s)
+    b = ops.gemv(x, Wq.view(torch.uint8), w_scale=s)
+    assert torch.equal(a, b)
+
+
 # ------------------------------------------------------------------- F4
 def f4_inputs(B, Hq, Hkv, L, seed):
     gen = torch.Generator().manual_seed(seed)
@@ -255,6 +344,68 @@ def test_f4_gqa_equals_mha_on_gpu():
     Vr = V.repeat_interleave(4, dim=1).contiguous()
     mha = ops.f4_flashdecode(q.cuda(), Kr.cuda(), Vr.cuda())
     assert rel_l2(gqa.float().cpu().numpy(), mha.float().cpu().numpy()) < 1e-3
+
+
+# ------------------------------------------------- decode-layer chain
+def c_oracle_layer(inp, Hq, fp8):
+    """The chain on the C oracle: fp16 rounding at every stage boundary (as
+    the torch stages round), each stage computed in double."""
+    np_ = {k: (v.view(torch.uint8).numpy() if v.dtype == torch.float8_e4m3fn else v.numpy())
+           for k, v in inp.items()}
+
+    def proj(a, key, skey):
+        if fp8:
+            return cref.f2h(cref.gemv_fp8_exact(a, np_[key], np_[skey]))
+        return cref.gemv(a, np_[key])
+
+    B = np_["x"].shape[0]
+    qkv = proj(cref.rmsnorm(np_["x"], np_["g1"]), "Wqkv", "s_qkv")
+    q = np.ascontiguousarray(qkv[:, : Hq * 128].reshape(B, Hq, 128))
+    attn = cref.f2h(cref.attention(q, np_["K"], np_["V"])).reshape(B, Hq * 128)
+    h = proj(attn, "Wo", "s_o")
+    hn = cref.rmsnorm(h, np_["g2"])
+    if fp8:
+        g = cref.f2h(cref.gemv_fp8_exact(hn, np_["Wg"], np_["s_gate"]))
+        u = cref.f2h(cref.gemv_fp8_exact(hn, np_["Wu"], np_["s_up"]))
+        ff = cref.swiglu(g, u)
+    else:
+        ff = cref.f2(hn, np_["Wg"], np_["Wu"])
+    return proj(ff, "Wd", "s_down").astype(np.float64)
+
+
+@pytest.mark.parametrize("dtype,B,L", [("f16", 1, 1024), ("fp8", 1, 1024), ("f16", 2, 520),
+                                       ("fp8", 3, 300)])
+def test_decode_layer_chain_parity(dtype, B, L):
+    """Config-5 chain at Llama-3-8B width through the fused HIP kernels
+    (F1 -> F4 -> O GEMV -> RMSNorm+F2 -> down GEMV) against the torch stage
+    chain on the CPU and against the C oracle chain.
+
+    Bar: each kernel meets rtol/atol 1e-2 on its own (the tests above); the
+    twelve fp16 rounding points of the chain compound, and the second
+    RMSNorm rescales the small O-projection output back to unit size, so two
+    valid implementations of the chain already differ by more: the torch
+    stages and the C oracle chain (same rounding points, double arithmetic
+    per stage) differ by up to 1.6e-2 and miss rtol/atol 1e-2 at 1-3 of 4096
+    outputs for these seeds.  The chain is held to rtol/atol 2e-2 against
+    both, and to rel-L2 <= 5e-3 against the C oracle chain."""
+    from decodebench_amd.demos.llama_decode import build_config
+
+    print(f"[layer] {dtype} B={B} L={L}", flush=True)
+    case = build_config("layer", batch=B, L=L, device="cpu", replicas=1, dtype=dtype,
+                        seed=700 + B + L)
+    cpu = case.inputs
+    gpu = {k: v.cuda() for k, v in cpu.items()}
+    y = case.fused(gpu)
+    torch.cuda.synchronize()
+    assert y.shape == (B, 4096)
+    fp8 = dtype == "fp8"
+    scales = ({k: cpu["s_" + k] for k in ("qkv", "o", "gate", "up", "down")} if fp8 else None)
+    ref = stages.decode_layer(cpu["x"], cpu["g1"], cpu["Wqkv"], cpu["K"], cpu["V"], cpu["Wo"],
+                              cpu["g2"], cpu["Wg"], cpu["Wu"], cpu["Wd"], 32, scales=scales)
+    exact = c_oracle_layer(cpu, 32, fp8)
+    assert_parity(y, ref, exact, 5e-3, f"layer {dtype} B={B} L={L}", tol=CHAIN_TOL)
+    got = y.float().cpu().numpy().astype(np.float64)
+    assert np.isclose(got, exact, rtol=CHAIN_TOL, atol=CHAIN_TOL).all()
 
 
 # ------------------------------------------------------------ graph replay

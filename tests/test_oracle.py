@@ -314,6 +314,34 @@ def test_fp8_gemv_dequant_then_gemv_equals_gemv_then_scale():
     assert rel_l2(cref.gemv_fp8_exact(x, Wq, scale), want) < 1e-12
 
 
+def test_e4m3_row_quantiser_and_fp8_stage():
+    """quantize_e4m3_rows maps each row's absmax onto 448 (3 mantissa bits:
+    relative error <= 2^-4 on normal values); the torch fp8 stage equals the
+    exact C oracle to fp16 rounding, and dropping the row scale is caught."""
+    torch = pytest.importorskip("torch")
+    from decodebench_amd.quant import dequantize_e4m3_rows, quantize_e4m3_rows
+    from oracle import stages
+
+    r = rng(14)
+    W = (r.standard_normal((96, 512)) * 0.02).astype(np.float16)
+    W[3] = 0
+    Wq, s = quantize_e4m3_rows(torch.from_numpy(W))
+    assert Wq.dtype == torch.float8_e4m3fn and s.dtype == torch.float32
+    live = np.arange(96) != 3
+    assert torch.all(Wq.float().abs().amax(1)[live] == 448.0)
+    assert float(s[3]) == 1.0 and torch.all(Wq[3].float() == 0)
+    deq = dequantize_e4m3_rows(Wq, s).numpy().astype(np.float64)
+    w64 = W.astype(np.float64)
+    normal = np.abs(w64) >= s.numpy()[:, None].astype(np.float64) * 2.0 ** -6
+    assert np.all(np.abs(deq - w64)[normal] <= np.abs(w64[normal]) * 2.0 ** -4 * (1 + 1e-6))
+    x = r.standard_normal((2, 512)).astype(np.float16)
+    got = stages.gemv_fp8(torch.from_numpy(x), Wq, s).float().numpy()
+    exact = cref.gemv_fp8_exact(x, Wq.view(torch.uint8).numpy(), s.numpy())
+    assert rel_l2(got, exact) < 1e-3
+    unscaled = (torch.from_numpy(x).float() @ Wq.float().T).numpy()
+    assert rel_l2(unscaled, exact) > 0.5
+
+
 # -------------------------------------------------- torch-stage restatement
 def test_torch_stages_match_c_oracle():
     torch = pytest.importorskip("torch")
