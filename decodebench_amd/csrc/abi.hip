@@ -255,6 +255,10 @@ int db_tune(const char* key, int value) {
     if (value != 0 && value != 4 && value != 8)
       return fail(DB_ERR_INVALID, "db_tune: f4_waves must be 0, 4 or 8");
     t.f4_waves = value;
+  } else if (!strcmp(key, "f4_merge")) {
+    if (value != 0 && value != 1)
+      return fail(DB_ERR_INVALID, "db_tune: f4_merge must be 0 or 1");
+    t.f4_merge = value;
   } else if (!strcmp(key, "f4_min_tiles")) {
     if (value < 1) return fail(DB_ERR_INVALID, "db_tune: f4_min_tiles must be >= 1");
     t.f4_min_tiles = value;

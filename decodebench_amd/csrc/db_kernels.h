@@ -14,6 +14,7 @@ struct Tuning {
   int f4_blocks_per_cu = 1;    // target F4 workgroups per CU
   int f4_min_tiles = 2;        // minimum 16-row tiles per F4 split
   int f4_waves = 0;            // waves per F4 workgroup (4 or 8; 0: auto)
+  int f4_merge = 0;            // 0: merge splits in a second launch; 1: same launch
 };
 Tuning& tuning();
 

@@ -29,11 +29,22 @@
 //    cross-lane reduction at the end.
 //  * The waves merge through LDS.  With S = 1 the workgroup writes the fp16
 //    output.  With S > 1 splits each workgroup writes an unnormalised partial
-//    (o, and the pair (m, l) per head) and a second, small launch merges the
-//    S partials of every (pair, head) by log-sum-exp.  The kernel boundary
-//    orders the partial stores before the merge loads; an in-kernel
-//    "last workgroup merges" scheme needs an L2 writeback plus a
-//    device-scope atomic per workgroup, which measured slower on MI355X.
+//    (o, and the pair (m, l) per head), and the S partials of every
+//    (pair, head) are merged by log-sum-exp in one of two ways:
+//      - in a second, small launch (f4_combine), ordered by the kernel
+//        boundary (the default);
+//      - in the same launch (db_tune "f4_merge" = 1): the partials are
+//        written with agent-coherent (sc1) stores; after waiting for them the
+//        workgroup takes a ticket from its pair's counter in the workspace
+//        with one relaxed atomic add, and the workgroup that draws the last
+//        ticket reads every partial with agent-coherent loads, merges, writes
+//        the output and resets the counter to zero.  No L2 writeback and no
+//        waiting on other workgroups is involved: the stores a ticket follows
+//        have completed at the agent's coherence point before the ticket is
+//        taken.  Its critical path holds three serial trips to that point
+//        (write-through stores, ticket, coherent loads), which measured
+//        1.9-2.4 us slower on MI355X than the launch boundary of the second
+//        launch (L = 1024 and 8192, batch 1).
 //
 // The merge follows the reference's two-phase split-KV form
 // (validation/src/kernels/fused/f4.cu:160-319): per-split max m, exp-sum l
@@ -63,8 +74,10 @@ struct F4Args {
   const _Float16* k;   // [B, Hkv, L, D]
   const _Float16* v;   // [B, Hkv, L, D]
   _Float16* o;         // [B, Hq, D]
+  unsigned* ticket;    // [B * Hkv]          split tickets (zero between calls)
   float2* ml;          // [B * Hkv, G, S]    (max, exp-sum) per split, base 2
   float* opart;        // [B * Hkv, S, G, D] unnormalised outputs
+  int fused_merge;     // 1: the last split of a pair merges in this launch
   int B, Hq, Hkv, L, S;
   int ntiles;          // ceil(L / 16)
   int tps;             // tiles per split
@@ -81,6 +94,16 @@ __device__ __forceinline__ float weight2(float m, float M) {
   return m == kNegInf ? 0.0f : fast_exp2(m - M);
 }
 
+// Agent-coherent accesses of the split partials (sc1 stores and loads on
+// gfx950, what relaxed agent-scope atomics compile to): a store is visible
+// device-wide once it has completed, and a load never returns a stale line
+// of another XCD's partials.  kSc1 is the sc1 cache-policy bit of a buffer
+// load.
+constexpr int kSc1 = 16;
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int G, int NW>
 __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
   static_assert(G >= 1 && G <= 8, "query heads per KV head");
@@ -90,6 +113,8 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
   __shared__ __align__(16) float s_o[NW][G][kD];  // per-wave outputs
   __shared__ float s_m[NW][G];
   __shared__ float s_l[NW][G];
+  // in-launch split merge: per split group and float4 slot (M, L, o[4])
+  __shared__ float s_merge[NW * kWave / (G * kD / 4)][G * kD / 4][6];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
@@ -276,13 +301,106 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
     }
     if (a.S == 1) {
       a.o[q_base + (size_t)h * kD + d] = to_h(ow / lw);
+    } else if (a.fused_merge) {
+      store_coherent(&a.opart[(((size_t)pair * a.S + split) * G + h) * kD + d], ow);
+      if (d == 0) {
+        float* mlp = reinterpret_cast<float*>(&a.ml[((size_t)pair * G + h) * a.S + split]);
+        store_coherent(mlp, M);
+        store_coherent(mlp + 1, lw);
+      }
     } else {
       a.opart[(((size_t)pair * a.S + split) * G + h) * kD + d] = ow;
       if (d == 0) a.ml[((size_t)pair * G + h) * a.S + split] = make_float2(M, lw);
     }
   }
-  if (a.S == 1) return;
+  if (a.S == 1 || !a.fused_merge) return;
 
+  // ---- ticket: the last split of the pair to finish merges ---------------
+  __shared__ unsigned s_last;
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned t = __hip_atomic_fetch_add(&a.ticket[pair], 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (t == (unsigned)(a.S - 1)) ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!s_last) return;
+
+  // Merge: thread (grp, slot) owns float4 slot `slot` of the G x D outputs
+  // and the splits grp, grp + kGrp, ...; all loads of a chunk of 8 splits are
+  // issued at once (agent-coherent 16- and 8-byte buffer loads), so S <= 8 kGrp
+  // costs one round trip.  The split groups then meet in LDS.
+  {
+    constexpr int kSlots = G * kD / 4;
+    constexpr int kGrp = kThreads / kSlots;  // >= 1: kThreads >= 256 >= kSlots
+    const int slot = threadIdx.x % kSlots, grp = threadIdx.x / kSlots;
+    const int h = slot / (kD / 4), d4 = slot % (kD / 4);
+    const __amdgpu_buffer_rsrc_t r_ml =
+        make_rsrc(a.ml + (size_t)pair * G * a.S, G * a.S * (int)sizeof(float2));
+    const __amdgpu_buffer_rsrc_t r_op =
+        make_rsrc(a.opart + (size_t)pair * a.S * G * kD, a.S * G * kD * (int)sizeof(float));
+    float M = kNegInf, Ls = 0.0f;
+    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (grp < kGrp) {
+      for (int s0 = grp; s0 < a.S; s0 += 8 * kGrp) {
+        f4 ov[8];
+        float2 mv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          // splits past S read zero bytes (out of the buffer's range)
+          const int sj = s0 + j * kGrp;
+          ov[j] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             r_op, ((sj * G + h) * kD + 4 * d4) * 4, 0, kSc1));
+          mv[j] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                 r_ml, (h * a.S + sj) * 8, 0, kSc1));
+          if (sj >= a.S) mv[j].x = kNegInf;
+        }
+        float Mn = M;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) Mn = fmaxf(Mn, mv[j].x);
+        const float r = weight2(M, Mn);
+        Ls *= r;
+        acc *= r;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float w = weight2(mv[j].x, Mn);
+          Ls = fmaf(w, mv[j].y, Ls);
+          acc += w * ov[j];
+        }
+        M = Mn;
+      }
+      float* c = &s_merge[grp][slot][0];
+      c[0] = M;
+      c[1] = Ls;
+      c[2] = acc[0];
+      c[3] = acc[1];
+      c[4] = acc[2];
+      c[5] = acc[3];
+    }
+    __syncthreads();
+    if (grp == 0) {
+      float Mt = kNegInf;
+#pragma unroll
+      for (int gi = 0; gi < kGrp; ++gi) Mt = fmaxf(Mt, s_merge[gi][slot][0]);
+      float Lt = 0.0f;
+      f4 at = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int gi = 0; gi < kGrp; ++gi) {
+        const float* cc = s_merge[gi][slot];
+        const float w = weight2(cc[0], Mt);
+        Lt = fmaf(w, cc[1], Lt);
+        at += w * f4{cc[2], cc[3], cc[4], cc[5]};
+      }
+      const float inv = 1.0f / Lt;
+      uint2 packed;
+      packed.x = pack_h2(at[0] * inv, at[1] * inv);
+      packed.y = pack_h2(at[2] * inv, at[3] * inv);
+      *reinterpret_cast<uint2*>(a.o + q_base + (size_t)h * kD + (size_t)d4 * 4) = packed;
+    }
+  }
+  if (threadIdx.x == 0)
+    __hip_atomic_store(&a.ticket[pair], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Second launch of a split call: one workgroup per (pair, query head).
@@ -390,10 +508,13 @@ int f4_max_splits(int G) {
   return 256;
 }
 
+// Workspace: [tickets: pairs x u32][ml: pairs x G x S float2][opart], each
+// region 256-byte aligned.
 size_t f4_workspace_bytes(int B, int Hq, int Hkv, int S, int D) {
   const int G = Hq / Hkv;
   const size_t pairs = (size_t)B * Hkv;
-  return round256(pairs * G * S * sizeof(float2)) + pairs * S * G * D * sizeof(float);
+  return round256(pairs * sizeof(unsigned)) + round256(pairs * G * S * sizeof(float2)) +
+         pairs * S * G * D * sizeof(float);
 }
 
 int f4_choose_splits(int B, int Hkv, int L, int cu_count) {
@@ -430,16 +551,19 @@ hipError_t launch_f4(const void* q, const void* k, const void* v, void* o,
   // The partial areas are laid out for the caller's S (the size it
   // allocated); the kernels use the first a.S <= S records of each pair.
   char* base = static_cast<char*>(ws);
-  a.ml = reinterpret_cast<float2*>(base);
-  a.opart = base ? reinterpret_cast<float*>(base + round256((size_t)pairs * G * S * sizeof(float2)))
-                 : nullptr;
+  const size_t ticket_bytes = round256((size_t)pairs * sizeof(unsigned));
+  const size_t ml_bytes = round256((size_t)pairs * G * S * sizeof(float2));
+  a.ticket = reinterpret_cast<unsigned*>(base);
+  a.ml = base ? reinterpret_cast<float2*>(base + ticket_bytes) : nullptr;
+  a.opart = base ? reinterpret_cast<float*>(base + ticket_bytes + ml_bytes) : nullptr;
+  a.fused_merge = tuning().f4_merge;
   a.xcd_map = (pairs % 8 == 0) ? 1 : 0;
   a.scale_log2 = scale * kLog2e;
   (void)D;
   int waves = tuning().f4_waves > 0 ? tuning().f4_waves : (a.tps >= 16 ? 8 : 4);
   hipLaunchKernelGGL(pick_kernel(G, waves), dim3(pairs * a.S), dim3(waves * kWave), 0,
                      stream, a);
-  if (a.S > 1) {
+  if (a.S > 1 && !a.fused_merge) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(f4_combine, dim3(pairs * G), dim3(256), 0, stream, a, G);

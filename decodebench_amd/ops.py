@@ -256,9 +256,10 @@ def f4_default_splits(B: int, Hkv: int, L: int, device=None) -> int:
 def f4_workspace(B: int, Hq: int, Hkv: int, L: int, D: int, S: int, device):
     """Workspace for db_f4_splitkv, cached per size and device.
 
-    The library needs no initialisation of it and keeps nothing in it between
-    calls, so one buffer serves every later call of that size on that device
-    (calls sharing it must not overlap in time)."""
+    It is zero-filled once, when allocated; every call leaves its split
+    tickets at zero again, so one buffer serves every later call of that size
+    on that device, also under graph capture (calls sharing it must not
+    overlap in time)."""
     import torch
 
     nbytes = int(load_library().db_f4_workspace_bytes(B, Hq, Hkv, L, D, S))
@@ -268,14 +269,14 @@ def f4_workspace(B: int, Hq: int, Hkv: int, L: int, D: int, S: int, device):
     key = (dev.index if dev.index is not None else torch.cuda.current_device(), nbytes)
     ws = _ws_cache.get(key)
     if ws is None:
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
         _ws_cache[key] = ws
     return ws
 
 
 def f4_flashdecode(q, K, V, scale: float | None = None, n_splits: int | None = None,
                    workspace=None):
-    """F4: split-KV GQA decode attention with the LSE combine, one launch.
+    """F4: split-KV GQA decode attention with the log-sum-exp merge.
 
     q [B,Hq,D], K/V [B,Hkv,L,D] fp16 (D = 128); query head h reads KV head
     h // (Hq // Hkv).  ``scale`` defaults to 1/sqrt(D); ``n_splits`` defaults

@@ -114,8 +114,10 @@ int db_gemv(const void* x, const void* W, const float* w_scale, void* y,
 int db_f4_default_splits(int B, int Hkv, int L, int cu_count);
 
 /* Bytes of caller-owned workspace db_f4_splitkv needs for S splits (0 when
- * S == 1): the per-split partial records.  Its contents need no
- * initialisation and are not needed after the call. */
+ * S == 1): one split ticket per (batch, kv-head) pair, then the per-split
+ * partial records.  The workspace must be zero-filled before its first use;
+ * every call leaves the tickets at zero again, so a workspace is zeroed once
+ * and then reused by any number of calls (including graph replays). */
 size_t db_f4_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S);
 
 /* F4: o[b,h,:] = softmax(scale * q[b,h,:] . K[b,h/G,:,:]^T) . V[b,h/G,:,:]
@@ -123,7 +125,8 @@ size_t db_f4_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S);
  * softmax and accumulation, fp16 output.  The KV length is cut into S splits
  * whose partial (max, exp-sum, unnormalised output) records go to the
  * workspace; a second launch on the same stream merges them by log-sum-exp
- * (one launch in total when S == 1).
+ * (one launch in total when S == 1; db_tune "f4_merge" = 1 lets the last
+ * split of each pair merge in the first launch instead).
  * Replaces f4_partial_kernel + f4_reduce_kernel
  * (validation/src/kernels/fused/f4.cu:173-319) and the reference stages
  * scores, softmax, weighted_v (src/decodebench/demos/llama_decode.py:120-134).
@@ -134,10 +137,11 @@ int db_f4_splitkv(const void* q, const void* k, const void* v, void* o,
                   void* ws, size_t ws_bytes, int B, int Hq, int Hkv, int L,
                   int D, int S, float scale, void* stream);
 
-/* Launch-geometry knobs for tuning sweeps ("gemv_waves_per_cu",
- * "gemv_mfma_min_batch", "f4_blocks_per_cu", "f4_min_tiles", "f4_waves"); value <= 0 restores the
- * default for the GEMV knob, 0 for "f4_waves" (4 or 8 waves per workgroup).
- * No counterpart in the reference. */
+/* Launch-geometry knobs for tuning sweeps: "gemv_waves_per_cu" (<= 0: the
+ * default choice), "gemv_mfma_min_batch", "f4_blocks_per_cu", "f4_min_tiles",
+ * "f4_waves" (4 or 8 waves per workgroup, 0: automatic) and "f4_merge" (0: the
+ * split merge runs in a second launch, the default; 1: in the same launch).
+ * Process-wide; no counterpart in the reference. */
 int db_tune(const char* key, int value);
 
 #ifdef __cplusplus

@@ -134,7 +134,7 @@ def test_f4_contract_errors(lib):
 def test_f4_workspace_and_split_policy(lib):
     assert lib.db_f4_workspace_bytes(1, 32, 8, 8192, 128, 1) == 0
     ws = lib.db_f4_workspace_bytes(1, 32, 8, 8192, 128, 64)
-    assert ws >= 8 * 64 * 4 * 130 * 4              # o, m, l per (pair, split, head)
+    assert ws >= 8 * 4 + 8 * 64 * 4 * 130 * 4      # tickets; o, m, l per (pair, split, head)
     s = lib.db_f4_default_splits(1, 8, 8192, 256)
     assert 1 <= s <= 256
     assert lib.db_f4_default_splits(1, 8, 16, 256) == 1       # one tile -> one split
@@ -145,6 +145,8 @@ def test_tune_keys(lib):
     assert lib.db_tune(b"nope", 1) == -1
     assert lib.db_tune(b"f4_blocks_per_cu", 0) == -1
     assert lib.db_tune(b"f4_waves", 5) == -1
+    assert lib.db_tune(b"f4_merge", 2) == -1
+    assert lib.db_tune(b"f4_merge", 0) == 0
     assert lib.db_tune(b"f4_blocks_per_cu", 2) == 0
     assert lib.db_tune(b"f4_blocks_per_cu", 1) == 0   # back to the default
 

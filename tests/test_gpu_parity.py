@@ -319,14 +319,16 @@ def test_f4_full_batch_split_invariance(L):
 
 
 def test_f4_workspace_reuse_is_deterministic():
-    """One workspace serves any number of calls: repeated calls (and a
-    different split count on the same workspace, whose stale records must not
-    leak into the result) give bitwise-identical results; a workspace full of
-    garbage (NaN bytes) before the first call changes nothing."""
+    """One zero-filled workspace serves any number of calls: repeated calls
+    (and a different split count on the same workspace, whose stale records
+    must not leak into the result) give bitwise-identical results; partial
+    records full of garbage (NaN bytes) before the first call change nothing;
+    every call leaves the split tickets at zero."""
     q, K, V = f4_inputs(1, 32, 8, 8192, 5)
     qd, Kd, Vd = q.cuda(), K.cuda(), V.cuda()
     nbytes = ops.load_library().db_f4_workspace_bytes(1, 32, 8, 8192, 128, 64)
     ws = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device="cuda")
+    ws[:256] = 0                        # the tickets of the 8 pairs (one 256-byte region)
     first = ops.f4_flashdecode(qd, Kd, Vd, n_splits=64, workspace=ws)
     for _ in range(20):
         again = ops.f4_flashdecode(qd, Kd, Vd, n_splits=64, workspace=ws)
@@ -335,6 +337,33 @@ def test_f4_workspace_reuse_is_deterministic():
     assert rel_l2(other.float().cpu().numpy(), first.float().cpu().numpy()) < 2e-3
     exact = cref.attention(q.numpy(), K.numpy(), V.numpy())
     assert rel_l2(first.float().cpu().numpy(), exact) < F4_REL_L2
+    torch.cuda.synchronize()
+    assert int(ws[:256].count_nonzero()) == 0
+
+
+@pytest.mark.parametrize("B,L", [(1, 1024), (1, 8192), (4, 8192), (8, 300)])
+def test_f4_in_launch_merge_matches_two_launch_merge(B, L):
+    """The split merge done by the last split's workgroup (f4_merge = 1) and
+    by a second launch (the default) agree to fp32 summation order, and 100
+    back-to-back calls of the in-launch merge are bitwise identical (the
+    ticket of every pair is taken exactly once per call and reset)."""
+    print(f"[f4-merge] B={B} L={L}", flush=True)
+    q, K, V = f4_inputs(B, 32, 8, L, 90 + B + L)
+    qd, Kd, Vd = q.cuda(), K.cuda(), V.cuda()
+    lib = ops.load_library()
+    two = ops.f4_flashdecode(qd, Kd, Vd)
+    try:
+        assert lib.db_tune(b"f4_merge", 1) == 0
+        one = ops.f4_flashdecode(qd, Kd, Vd)
+        outs = [ops.f4_flashdecode(qd, Kd, Vd) for _ in range(100)]
+        torch.cuda.synchronize()
+    finally:
+        assert lib.db_tune(b"f4_merge", 0) == 0
+    assert rel_l2(one.float().cpu().numpy(), two.float().cpu().numpy()) < 1e-3
+    for o in outs:
+        assert torch.equal(o, one)
+    exact = cref.attention(q.numpy(), K.numpy(), V.numpy())
+    assert rel_l2(one.float().cpu().numpy(), exact) < F4_REL_L2
 
 
 def test_f4_gqa_equals_mha_on_gpu():
