@@ -246,7 +246,8 @@ int db_tune(const char* key, int value) {
   if (!strcmp(key, "gemv_waves_per_cu")) {
     t.gemv_waves_per_cu = value > 0 ? value : 0;
   } else if (!strcmp(key, "gemv_mfma_min_batch")) {
-    if (value < 2) return fail(DB_ERR_INVALID, "db_tune: gemv_mfma_min_batch must be >= 2");
+    if (value < 0 || value == 1)
+      return fail(DB_ERR_INVALID, "db_tune: gemv_mfma_min_batch must be 0 (automatic) or >= 2");
     t.gemv_mfma_min_batch = value;
   } else if (!strcmp(key, "f4_blocks_per_cu")) {
     if (value < 1) return fail(DB_ERR_INVALID, "db_tune: f4_blocks_per_cu must be >= 1");

@@ -124,11 +124,12 @@ def test_plain_gemv_parity():
 
 
 # --------------------------------------------------- batched GEMV (MFMA)
-# Batches of 2 and more with K in {2048, 4096} take the MFMA kernel: ragged
-# batches (one and two 16-row passes), N not a multiple of the 8-row group.
+# Batches from 3 rows (one weight matrix) or 5 rows (gate/up pair) with K in
+# {2048, 4096} take the MFMA kernel: ragged batches (one and two 16-row
+# passes), N not a multiple of the 8-row group.
 MFMA_CASES = [
-    ("f1", 2, 4096, 1000), ("f1", 17, 4096, 6144), ("f1", 32, 2048, 1032),
-    ("f2", 4, 4096, 14336), ("f2", 32, 4096, 1792), ("f2", 9, 2048, 777),
+    ("f1", 3, 4096, 1000), ("f1", 17, 4096, 6144), ("f1", 32, 2048, 1032),
+    ("f2", 5, 4096, 14336), ("f2", 32, 4096, 1792), ("f2", 9, 2048, 777),
     ("plain", 16, 4096, 4100), ("plain", 3, 2048, 8),
 ]
 
@@ -175,7 +176,7 @@ def test_mfma_and_valu_gemv_paths_agree():
             outs.append((ops.f1_rmsnorm_gemv(x, g, W), ops.f2_gateup_swiglu(x, W, Wu),
                          ops.gemv(x, W)))
     finally:
-        lib.db_tune(b"gemv_mfma_min_batch", 2)
+        lib.db_tune(b"gemv_mfma_min_batch", 0)
     for a, b in zip(*outs):
         assert rel_l2(a.float().cpu().numpy(), b.float().cpu().numpy()) < 1e-3
 
