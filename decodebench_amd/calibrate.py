@@ -1,0 +1,173 @@
+"""Calibration on one MI355X: launch overhead and the G2 GEMV gate.
+
+The counterpart of the reference's ``calibrate`` harness
+(validation/src/bench/calibrate.cu:42-230):
+
+* :func:`null_launch` -- an empty kernel (``db_null_kernel``) launched 500
+  times on a stream, and a one-kernel hipGraph replayed 500 times, both timed
+  with events (calibrate.cu:42-104).  It adds one MI355X figure: the cost of
+  an empty kernel back to back inside one graph, the floor every fused call
+  pays per launch.
+* :func:`gate_g2` -- the plain fp16 GEMV of this library (``db_gemv``)
+  against the vendor BLAS at the FFN shape W[14336, 4096]
+  (calibrate.cu:113-230): on ROCm ``F.linear`` dispatches to hipBLASLt /
+  rocBLAS, the role cuBLAS plays there.  G2 passes when ours reaches at
+  least 90% of the vendor bandwidth.  Inputs are uniform: W in +-0.02, x in
+  +-1 (calibrate.cu:137-140).  The reference times one weight matrix over
+  and over; 117 MB fits the MI355X's 256 MB Infinity Cache, so by default
+  both sides here rotate over cache-defeating weight replicas
+  (``rotate=False`` gives the reference's single-matrix loop).
+
+The printed lines follow calibrate.cu's output ("t_launch_stream: ... us",
+"G2: PASS"), with the vendor line labelled by the library that ran.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+
+@dataclass
+class NullLaunch:
+    t_launch_stream_us: float   # eager launches, events around 500 of them
+    t_launch_graph_us: float    # replays of a one-kernel graph
+    t_kernel_in_graph_us: float  # one kernel of 500 back to back in one graph
+
+    def render(self) -> str:
+        return (f"t_launch_stream: {self.t_launch_stream_us:.2f} us\n"
+                f"t_launch_graph:  {self.t_launch_graph_us:.2f} us\n"
+                f"t_kernel_in_graph: {self.t_kernel_in_graph_us:.2f} us")
+
+
+@dataclass
+class GateG2:
+    d_out: int
+    d_in: int
+    us_ours: float
+    us_vendor: float
+    gbs_ours: float
+    gbs_vendor: float
+    replicas: int
+    vendor: str
+    max_abs_diff: float
+
+    @property
+    def ratio(self) -> float:
+        return self.gbs_ours / self.gbs_vendor
+
+    @property
+    def passed(self) -> bool:
+        return self.ratio >= 0.90
+
+    def render(self) -> str:
+        return (f"GEMV d_out={self.d_out} d_in={self.d_in} ({self.replicas} weight replica"
+                f"{'s' if self.replicas != 1 else ''})\n"
+                f"  Ours:   {self.us_ours:.2f} us  ({self.gbs_ours:.2f} GB/s)\n"
+                f"  {self.vendor}: {self.us_vendor:.2f} us  ({self.gbs_vendor:.2f} GB/s)\n"
+                f"  Ratio (ours/{self.vendor}): {self.ratio * 100.0:.1f}%\n"
+                f"G2: {'PASS' if self.passed else 'FAIL'}")
+
+
+def _events():
+    import torch
+
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def null_launch(iters: int = 500) -> NullLaunch:
+    import torch
+
+    from decodebench_amd import ops
+
+    ops.load_library()
+    ops.null_kernel()
+    torch.cuda.synchronize()
+    e0, e1 = _events()
+    e0.record()
+    for _ in range(iters):
+        ops.null_kernel()
+    e1.record()
+    torch.cuda.synchronize()
+    t_stream = e0.elapsed_time(e1) * 1e3 / iters
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    one, many = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        ops.null_kernel()
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(one):
+        ops.null_kernel()
+    with torch.cuda.graph(many):
+        for _ in range(iters):
+            ops.null_kernel()
+    one.replay()
+    many.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(iters):
+        one.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    t_graph = e0.elapsed_time(e1) * 1e3 / iters
+    e0.record()
+    many.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    t_in_graph = e0.elapsed_time(e1) * 1e3 / iters
+    return NullLaunch(t_stream, t_graph, t_in_graph)
+
+
+def _vendor_name() -> str:
+    import torch
+
+    try:
+        backend = torch.backends.cuda.preferred_blas_library()
+        name = str(backend).split(".")[-1]
+    except Exception:  # older torch: no query
+        name = "blas"
+    return {"Cublaslt": "hipBLASLt", "Cublas": "rocBLAS", "Ck": "CK"}.get(name, name)
+
+
+def gate_g2(iters: int = 200, d_in: int = 4096, d_out: int = 14336, rotate: bool = True,
+            seed: int = 42) -> GateG2:
+    import torch
+    import torch.nn.functional as F
+
+    from decodebench_amd import ops
+    from decodebench_amd.timing import cache_defeat_replicas
+
+    ops.load_library()
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+
+    def uniform(shape, scale):
+        t = torch.rand(*shape, generator=gen, device="cuda", dtype=torch.float32)
+        return ((t * 2.0 - 1.0) * scale).half()
+
+    W = uniform((d_out, d_in), 0.02)
+    x = uniform((1, d_in), 1.0)
+    n = cache_defeat_replicas(W.nbytes) if rotate else 1
+    Ws = [W] + [W.clone() for _ in range(n - 1)]
+
+    ours = ops.gemv(x, W)
+    ref = F.linear(x, W)
+    torch.cuda.synchronize()
+    max_abs = float((ours.float() - ref.float()).abs().max())
+
+    def timed(fn) -> float:
+        for i in range(min(len(Ws), 8)):
+            fn(Ws[i % len(Ws)])
+        torch.cuda.synchronize()
+        e0, e1 = _events()
+        e0.record()
+        for i in range(iters):
+            fn(Ws[i % len(Ws)])
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / iters
+
+    us_ours = timed(lambda w: ops.gemv(x, w))
+    us_vendor = timed(lambda w: F.linear(x, w))
+    nbytes = 2.0 * (d_out * d_in + d_in + d_out)
+    return GateG2(d_out, d_in, us_ours, us_vendor, nbytes / (us_ours * 1e3),
+                  nbytes / (us_vendor * 1e3), n, _vendor_name(), max_abs)

@@ -135,6 +135,8 @@ int run_gemv(const char* fn, dbk::GemvMode mode, const void* x, const void* g,
                     fn);
 }
 
+__global__ void null_kernel() {}
+
 }  // namespace
 
 extern "C" {
@@ -238,6 +240,11 @@ int db_f4_splitkv(const void* q, const void* k, const void* v, void* o,
   return hip_status(dbk::launch_f4(q, k, v, o, ws, B, Hq, Hkv, L, D, S, scale,
                                    (hipStream_t)stream),
                     fn);
+}
+
+int db_null_kernel(void* stream) {
+  hipLaunchKernelGGL(null_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream);
+  return hip_status(hipGetLastError(), "db_null_kernel");
 }
 
 int db_tune(const char* key, int value) {

@@ -68,6 +68,7 @@ def load_library():
             "db_f4_splitkv": (_i, [_p, _p, _p, _p, _p, C.c_size_t, _i, _i, _i, _i, _i, _i,
                                    C.c_float, _p]),
             "db_tune": (_i, [C.c_char_p, _i]),
+            "db_null_kernel": (_i, [_p]),
         }
         for name, (res, args) in protos.items():
             fn = getattr(lib, name)
@@ -117,6 +118,16 @@ def cu_count(device=None) -> int:
     if idx not in _cu_cache:
         _cu_cache[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
     return _cu_cache[idx]
+
+
+def null_kernel(device=None) -> None:
+    """Launch the library's empty kernel on the current stream (the
+    launch-overhead probe of ``decodebench_amd.calibrate``)."""
+    import torch
+
+    dev = torch.device("cuda" if device is None else device)
+    _check(load_library().db_null_kernel(torch.cuda.current_stream(dev).cuda_stream),
+           "db_null_kernel")
 
 
 def tune(key: str, value: int) -> None:

@@ -137,6 +137,13 @@ int db_f4_splitkv(const void* q, const void* k, const void* v, void* o,
                   void* ws, size_t ws_bytes, int B, int Hq, int Hkv, int L,
                   int D, int S, float scale, void* stream);
 
+/* Launch an empty kernel (one workgroup of 256 threads) on `stream`: the
+ * launch-overhead probe of the calibration.  Replaces null_kernel and its
+ * 500-launch stream / graph timing loop (validation/src/bench/
+ * calibrate.cu:42-104), whose timing the Python calibration does with HIP
+ * events. */
+int db_null_kernel(void* stream);
+
 /* Launch-geometry knobs for tuning sweeps: "gemv_waves_per_cu" (<= 0: the
  * default, 32), "gemv_mfma_min_batch" (0: automatic, 3 for one weight matrix
  * and 5 for the gate/up pair), "f4_blocks_per_cu", "f4_min_tiles",
