@@ -113,8 +113,6 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
   __shared__ __align__(16) float s_o[NW][G][kD];  // per-wave outputs
   __shared__ float s_m[NW][G];
   __shared__ float s_l[NW][G];
-  // in-launch split merge: per split group and float4 slot (M, L, o[4])
-  __shared__ float s_merge[NW * kWave / (G * kD / 4)][G * kD / 4][6];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
@@ -334,6 +332,10 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
   {
     constexpr int kSlots = G * kD / 4;
     constexpr int kGrp = kThreads / kSlots;  // >= 1: kThreads >= 256 >= kSlots
+    // (M, L, o[4]) per split group and float4 slot, in the V-tile LDS, which
+    // no wave reads any more.
+    static_assert(sizeof(float) * kGrp * kSlots * 6 <= sizeof(s_v), "merge scratch");
+    auto s_merge = reinterpret_cast<float (*)[kSlots][6]>(&s_v[0][0][0]);
     const int slot = threadIdx.x % kSlots, grp = threadIdx.x / kSlots;
     const int h = slot / (kD / 4), d4 = slot % (kD / 4);
     const __amdgpu_buffer_rsrc_t r_ml =

@@ -62,12 +62,14 @@ using GemvFn = void (*)(GemvArgs);
 GemvFn gemv_pick_f16(GemvMode mode, int nb, int u);
 GemvFn gemv_pick_fp8(GemvMode mode, int nb, int u);
 
-// Rows per wave group: every tile keeps about 16 loads of 16 bytes in flight
-// per lane (R rows x U chunks x the one or two matrices).
+// Rows per wave group, measured on MI355X at the decode shapes: fp16 keeps
+// 16 loads of 16 bytes per lane per tile (2 rows x 8 chunks, or the gate/up
+// pair x 1 row); e4m3 rows are half as long, and 2 rows per group (8 loads
+// for one matrix, 16 for the pair) beat both 1 and 4 rows at K = 4096.
 constexpr int gemv_rows_per_group(int mode, bool fp8, int u) {
   const int nw = gemv_is_swiglu(mode) ? 2 : 1;
   if (!fp8) return nw == 2 ? 1 : 2;
-  return u <= 4 ? (nw == 1 ? 4 : 2) : (nw == 1 ? 2 : 1);
+  return u <= 4 ? 2 : (nw == 1 ? 2 : 1);
 }
 
 namespace {
