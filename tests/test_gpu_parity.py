@@ -181,6 +181,51 @@ def test_mfma_and_valu_gemv_paths_agree():
         assert rel_l2(a.float().cpu().numpy(), b.float().cpu().numpy()) < 1e-3
 
 
+# --------------------------------------------------- GEMV edge shapes
+# The smallest K (one 16-byte chunk per row), a single output row, and the
+# largest K the ABI accepts (the activation row fills the 152 KB LDS
+# budget), for fp16 and e4m3 weights.
+EDGE_CASES = [("f1", 1, 8, 1, "f16"), ("plain", 3, 8, 5, "f16"), ("f2", 2, 16, 1, "f16"),
+              ("f1", 1, 77824, 64, "f16"), ("plain", 1, 77824, 33, "fp8"),
+              ("f2", 1, 77824, 17, "fp8"), ("plain", 1, 16, 1, "fp8")]
+
+
+@pytest.mark.parametrize("mode,B,K,N,dtype", EDGE_CASES)
+def test_gemv_edge_shapes(mode, B, K, N, dtype):
+    from decodebench_amd.quant import quantize_e4m3_rows
+
+    print(f"[edge] {mode} {dtype} B={B} K={K} N={N}", flush=True)
+    gen = torch.Generator().manual_seed(7000 + B + K + N)
+    x = randn(gen, (B, K))
+    g = randn(gen, (K,), std=0.1, mean=1.0)
+    w_std = 1.0 / math.sqrt(K)
+    W, W2 = randn(gen, (N, K), std=w_std), randn(gen, (N, K), std=w_std)
+    xd, gd = x.cuda(), g.cuda()
+    if dtype == "fp8":
+        Wq, s = quantize_e4m3_rows(W)
+        W2q, s2 = quantize_e4m3_rows(W2)
+        bits, bits2 = Wq.view(torch.uint8).numpy(), W2q.view(torch.uint8).numpy()
+        if mode == "plain":
+            y = ops.gemv(xd, Wq.cuda(), w_scale=s.cuda())
+            ref, exact = stages.gemv_fp8(x, Wq, s), cref.gemv_fp8_exact(x.numpy(), bits, s.numpy())
+        else:
+            y = ops.f2_gateup_swiglu(xd, Wq.cuda(), W2q.cuda(), s.cuda(), s2.cuda())
+            ref = stages.f2_fp8(x, Wq, s, W2q, s2)
+            exact = cref.f2_fp8_exact(x.numpy(), bits, s.numpy(), bits2, s2.numpy())
+    elif mode == "f1":
+        y = ops.f1_rmsnorm_gemv(xd, gd, W.cuda())
+        ref, exact = stages.f1(x, g, W), cref.f1_exact(x.numpy(), g.numpy(), W.numpy())
+    elif mode == "f2":
+        y = ops.f2_gateup_swiglu(xd, W.cuda(), W2.cuda())
+        ref, exact = stages.f2(x, W, W2), cref.f2_exact(x.numpy(), W.numpy(), W2.numpy())
+    else:
+        y = ops.gemv(xd, W.cuda())
+        ref, exact = stages.gemv(x, W), cref.gemv_exact(x.numpy(), W.numpy())
+    torch.cuda.synchronize()
+    assert y.shape == (B, N)
+    assert_parity(y, ref, exact, 5e-3, f"edge {mode} {dtype} B={B} K={K} N={N}")
+
+
 # ------------------------------------------- RMSNorm -> gate/up + SwiGLU
 # One kernel for the decode chain's post-attention half; batch 1 takes the
 # VALU kernel, batches of 2..16 (and passes of 16) the MFMA kernel.
@@ -439,6 +484,31 @@ def test_decode_layer_chain_parity(dtype, B, L):
 
 
 # ------------------------------------------------------------ graph replay
+@pytest.mark.parametrize("dtype", ["f16", "fp8"])
+def test_decode_layer_replays_correctly_in_a_graph(dtype):
+    """The six launches of the decode layer captured into one graph: five
+    replays, with eager work in between, are bitwise equal to the eager
+    call (the F4 workspace needs no reset between replays)."""
+    from decodebench_amd.demos.llama_decode import build_config
+
+    case = build_config("layer", batch=1, L=2048, replicas=1, dtype=dtype, seed=31)
+    inp = case.inputs
+    eager = case.fused(inp).clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        case.fused(inp)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = case.fused(inp)
+    for i in range(5):
+        inp["x"].add_(0.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"{dtype} replay {i} differs from eager"
+
+
 def test_ops_replay_correctly_in_a_graph():
     gen = torch.Generator().manual_seed(11)
     x = randn(gen, (1, 4096)).cuda()
