@@ -562,7 +562,9 @@ hipError_t launch_f4(const void* q, const void* k, const void* v, void* o,
   a.xcd_map = (pairs % 8 == 0) ? 1 : 0;
   a.scale_log2 = scale * kLog2e;
   (void)D;
-  int waves = tuning().f4_waves > 0 ? tuning().f4_waves : (a.tps >= 16 ? 8 : 4);
+  // 8 waves once a split has a tile for each (measured: 10% faster than 4
+  // at batch 4, L = 1024, where a split holds 8 tiles); 4 below that.
+  int waves = tuning().f4_waves > 0 ? tuning().f4_waves : (a.tps >= 8 ? 8 : 4);
   hipLaunchKernelGGL(pick_kernel(G, waves), dim3(pairs * a.S), dim3(waves * kWave), 0,
                      stream, a);
   if (a.S > 1 && !a.fused_merge) {
