@@ -172,7 +172,11 @@ def sweep_workloads():
     # fp8 e4m3 weights (per-row scales) at batch 1, and the config-5 layer
     out += [("f1_cfg1_fp8", dict(name="f1", batch=1, dtype="fp8")),
             ("f1_qkv_cfg3_fp8", dict(name="f1_qkv", batch=1, dtype="fp8")),
-            ("f2_cfg2_fp8", dict(name="f2", batch=1, dtype="fp8")),
+            ("f2_cfg2_fp8", dict(name="f2", batch=1, dtype="fp8"))]
+    out += [(f"f1_qkv_cfg3_fp8_B{B}", dict(name="f1_qkv", batch=B, dtype="fp8"))
+            for B in (4, 8, 16, 32)]
+    out += [(f"f2_cfg2_fp8_B{B}", dict(name="f2", batch=B, dtype="fp8")) for B in (4, 16)]
+    out += [
             ("layer_cfg5", dict(name="layer", batch=1, L=8192)),
             ("layer_cfg5_fp8", dict(name="layer", batch=1, L=8192, dtype="fp8"))]
     return out

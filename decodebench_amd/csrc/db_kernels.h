@@ -12,7 +12,8 @@ struct Tuning {
   int gemv_waves_per_cu = 0;   // 0: the default, 32 waves per CU
   int gemv_mfma_min_batch = 0; // smallest batch that takes the MFMA GEMV
                                // (0: 3 for one weight matrix, 5 for the
-                               // gate/up pair -- the measured crossovers)
+                               // gate/up pair, 4 with e4m3 weights -- the
+                               // measured crossovers)
   int f4_blocks_per_cu = 1;    // target F4 workgroups per CU
   int f4_min_tiles = 2;        // minimum 16-row tiles per F4 split
   int f4_waves = 0;            // waves per F4 workgroup (4 or 8; 0: auto)
@@ -58,12 +59,12 @@ hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
                        const GemvWeights& w, void* y, int B, int K, int N, float eps,
                        int cu_count, hipStream_t stream);
 
-// MFMA variant for batches of 2..16 rows per pass (gemv_mfma.hip), fp16
-// weights only.
+// MFMA variant for batches of up to 16 rows per pass (gemv_mfma.hip), fp16
+// or e4m3 weights, K in {2048, 4096}.
 bool gemv_mfma_supported(int B, int K, int N);
 hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
-                            const void* w0, const void* w1, void* y, int B, int K,
-                            int N, float eps, int cu_count, hipStream_t stream);
+                            const GemvWeights& w, void* y, int B, int K, int N, float eps,
+                            int cu_count, hipStream_t stream);
 
 // Split-KV GQA decode attention with the log-sum-exp combine in-kernel.
 size_t f4_workspace_bytes(int B, int Hq, int Hkv, int S, int D);

@@ -2,7 +2,7 @@
 //
 // y[B,N] = op(x[B,K]) . W^T for the four GEMV modes of gemv.hip (plain,
 // RMSNorm-fused F1, gate/up + SwiGLU F2, RMSNorm -> gate/up + SwiGLU) with
-// fp16 weights when the batch is large enough that the VALU dot-product path
+// fp16 or e4m3 weights when the batch is large enough that the VALU dot-product path
 // becomes instruction-bound (at batch 8 it runs at a third of HBM speed).  The weights are still read exactly once; MFMA does
 // the multiply-adds.
 //
@@ -48,9 +48,11 @@ constexpr int kMaxGroupsPerWg = 8;   // LDS partial-sum slots per workgroup
 
 struct MfmaArgs {
   const _Float16* x;      // [B, K]
-  const _Float16* gamma;  // [K]     (RMSNorm mode)
-  const _Float16* w0;     // [N, K]  (gate in SwiGLU mode)
-  const _Float16* w1;     // [N, K]  (up, SwiGLU mode only)
+  const _Float16* gamma;  // [K]     (norm modes)
+  const void* w0;         // [N, K]  fp16 or e4m3 (gate in the SwiGLU modes)
+  const void* w1;         // [N, K]  (up, SwiGLU modes only)
+  const float* s0;        // [N]     e4m3 row scales of w0
+  const float* s1;        // [N]     e4m3 row scales of w1
   _Float16* y;            // [B, N]
   int B, K, N;
   int groups;             // ceil(N / 8)
@@ -63,9 +65,16 @@ struct MfmaArgs {
 // UPS: groups per register set.  When a workgroup's groups fit in one set
 // (UPS >= groups per workgroup) they are all requested before the prologue
 // and no loop runs; otherwise two sets alternate.
-template <int MODE, int KH, int BT, int UPS, bool SINGLE>
+// FP8: e4m3 weights.  A 16-byte load then holds 16 weights, the A operands
+// of two k-steps after v_cvt_scalef32_pk_f16_fp8 widening: step 2p + e of
+// lane group g4 covers columns 64 p + 16 g4 + 8 e of the half slice (for
+// fp16, step t covers 32 t + 8 g4).  The activations are loaded in the same
+// column order, so the dot products are unchanged; the row scales multiply
+// the reduced sums in the epilogue.
+template <int MODE, int KH, int BT, int UPS, bool SINGLE, bool FP8>
 __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   constexpr int NWM = gemv_is_swiglu(MODE) ? 2 : 1;
+  constexpr int KW = FP8 ? KH / 2 : KH;  // 16-byte weight loads per row and slice
   // [group][matrix][wave][batch][row]
   __shared__ __align__(16) float part[kMaxGroupsPerWg][NWM][kWavesM][kBatchTile][kRowsPerGroup];
   __shared__ float red[kWavesM][kBatchTile];
@@ -79,8 +88,14 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   const int half = c16 >> 3;  // which half of the slice this lane covers
   const int b0 = blockIdx.y * kBatchTile;
   const int nb = min(kBatchTile, a.B - b0);
-  // This lane's first column: the slice of wave v is [v, v+1) * K / 8.
-  const int kcol = wave * KH * 64 + half * KH * 32 + 8 * g4;
+  // The slice of wave v is [v, v+1) * K / 8; this lane's half starts at sbase.
+  const int sbase = wave * KH * 64 + half * KH * 32;
+  const int kcol = sbase + 8 * g4;  // fp16: this lane's column for k-step 0
+  // Column of this lane's activation chunk for k-step t.
+  auto xcol = [&](int t) {
+    if constexpr (FP8) return sbase + 64 * (t >> 1) + 16 * g4 + 8 * (t & 1);
+    return kcol + 32 * t;
+  };
 
   // ---- activation slice -> registers (B operand), loads unconditional ----
   // F1's gamma is shared by every batch row: thread t fetches 16-byte chunk t
@@ -92,7 +107,8 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   for (int bt = 0; bt < BT; ++bt) {
     const int xrow = b0 + min(8 * bt + r8, nb - 1);
 #pragma unroll
-    for (int t = 0; t < KH; ++t) xr[bt][t] = ld16(a.x + (size_t)xrow * a.K + kcol + 32 * t);
+    for (int t = 0; t < KH; ++t)
+      xr[bt][t] = ld16(a.x + (size_t)xrow * a.K + (FP8 ? xcol(t) : kcol + 32 * t));
   }
   u4 gchunk = {0, 0, 0, 0};
   if constexpr (gemv_has_norm(MODE))
@@ -102,10 +118,11 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   // ---- the workgroup's groups: rows of group j are 8 (w + grid j) .. +7 --
   const int my_groups = min(a.gpw, (a.groups - (int)blockIdx.x + (int)gridDim.x - 1) /
                                        (int)gridDim.x);
-  const _Float16* wmat[2] = {a.w0, a.w1};
+  const unsigned char* wmat[2] = {static_cast<const unsigned char*>(a.w0),
+                                  static_cast<const unsigned char*>(a.w1)};
   // `checked`: skip groups past my_groups (only outside the steady loop,
   // whose loads are unconditional so the compiler waits per set).
-  auto load_set = [&](u4 (&dst)[UPS][NWM][KH], int j0, bool checked) {
+  auto load_set = [&](u4 (&dst)[UPS][NWM][KW], int j0, bool checked) {
 #pragma unroll
     for (int q = 0; q < UPS; ++q) {
       if (checked && j0 + q >= my_groups) break;
@@ -114,12 +131,15 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
 #pragma unroll
       for (int m = 0; m < NWM; ++m)
 #pragma unroll
-        for (int t = 0; t < KH; ++t)
-          dst[q][m][t] = ld_stream(wmat[m] + (size_t)row * a.K + kcol + 32 * t);
+        for (int t = 0; t < KW; ++t)
+          dst[q][m][t] =
+              FP8 ? ld_stream(wmat[m] + (size_t)row * a.K + xcol(2 * t))
+                  : ld_stream(reinterpret_cast<const _Float16*>(wmat[m]) + (size_t)row * a.K +
+                              kcol + 32 * t);
     }
   };
 
-  u4 wa[UPS][NWM][KH];
+  u4 wa[UPS][NWM][KW];
   load_set(wa, 0, true);  // every workgroup owns at least one group
   __builtin_amdgcn_sched_barrier(0);
 
@@ -161,7 +181,7 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
       const float inv = 1.0f / sqrtf(tot / (float)a.K + a.eps);
 #pragma unroll
       for (int t = 0; t < KH; ++t) {
-        const u4 gv = s_gamma[(kcol + 32 * t) / 8];
+        const u4 gv = s_gamma[(FP8 ? xcol(t) : kcol + 32 * t) / 8];
         u4 out;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -177,21 +197,30 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   }
 
   // ---- stream the groups ------------------------------------------------
-  auto consume = [&](const u4 (&src)[UPS][NWM][KH], int j0) {
+  auto consume = [&](const u4 (&src)[UPS][NWM][KW], int j0) {
 #pragma unroll
     for (int q = 0; q < UPS; ++q) {
       const int j = j0 + q;
       if (j >= my_groups) break;
 #pragma unroll
       for (int m = 0; m < NWM; ++m) {
+        // e4m3: the A operands of the KH k-steps, widened to fp16 once per
+        // group; fp16: the loaded registers themselves.
+        u4 av[FP8 ? KH : 1];
+        if constexpr (FP8) {
+#pragma unroll
+          for (int t = 0; t < KW; ++t) e4m3x16_to_h(src[q][m][t], av[2 * t], av[2 * t + 1]);
+        }
 #pragma unroll
         for (int bt = 0; bt < BT; ++bt) {
           f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-          for (int t = 0; t < KH; ++t)
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, src[q][m][t]),
+          for (int t = 0; t < KH; ++t) {
+            const u4 at = FP8 ? av[FP8 ? t : 0] : src[q][m][FP8 ? 0 : t];
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, at),
                                                          __builtin_bit_cast(h8, xr[bt][t]), acc,
                                                          0, 0, 0);
+          }
           // D[4 g4 + i][c16]: rows 0..7 x columns 0..7 (half 0) live in lanes
           // (g4 < 2, c16 < 8); their half-1 partners sit 40 lanes higher.
 #pragma unroll
@@ -209,7 +238,7 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
     // Two register sets; the steady loop loads and consumes set B inside
     // one iteration (see flashdecode.hip for why that matters to the
     // compiler).
-    u4 wb[UPS][NWM][KH];
+    u4 wb[UPS][NWM][KW];
     int j = 0;
     for (; j + 3 * UPS <= my_groups; j += 2 * UPS) {
       load_set(wb, j + UPS, false);
@@ -241,6 +270,10 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
       s0 += part[jj][0][v][n][r];
       if constexpr (NWM == 2) s1 += part[jj][NWM - 1][v][n][r];
     }
+    if constexpr (FP8) {
+      s0 *= a.s0[row];
+      if constexpr (NWM == 2) s1 *= a.s1[row];
+    }
     float out;
     if constexpr (NWM == 2) {
       const float gq = (float)to_h(s0);
@@ -257,39 +290,49 @@ using MfmaFn = void (*)(MfmaArgs);
 
 // ups > 0: one set of `ups` groups holds all of a workgroup's groups;
 // ups < 0: alternating sets of -ups groups.
-template <int MODE, int KH, int BT>
+template <int MODE, int KH, int BT, bool FP8>
 MfmaFn pick_ups(int ups) {
   if constexpr (MODE == kGemvRmsNormSwiGLU && BT == 2) {
     // The normalisation next to two batch tiles and a gate/up pair: one
     // group pair per alternating set.
     (void)ups;
-    return gemv_mfma_kernel<MODE, KH, BT, 1, false>;
+    return gemv_mfma_kernel<MODE, KH, BT, 1, false, FP8>;
   } else if constexpr (gemv_is_swiglu(MODE)) {
-    return ups == 2 ? gemv_mfma_kernel<MODE, KH, BT, 2, true>
-                    : gemv_mfma_kernel<MODE, KH, BT, 1, false>;
+    return ups == 2 ? gemv_mfma_kernel<MODE, KH, BT, 2, true, FP8>
+                    : gemv_mfma_kernel<MODE, KH, BT, 1, false, FP8>;
   } else if constexpr (MODE == kGemvRmsNorm && BT == 2) {
     // Two batch tiles of F1 leave no registers for a whole-workgroup set
     // next to the normalisation; always alternate two sets of 2 groups.
     (void)ups;
-    return gemv_mfma_kernel<MODE, KH, BT, 2, false>;
+    return gemv_mfma_kernel<MODE, KH, BT, 2, false, FP8>;
   } else {
     switch (ups) {
-      case 2: return gemv_mfma_kernel<MODE, KH, BT, 2, true>;
-      case 3: return gemv_mfma_kernel<MODE, KH, BT, 3, true>;
-      case 4: return gemv_mfma_kernel<MODE, KH, BT, 4, true>;
-      default: return gemv_mfma_kernel<MODE, KH, BT, 2, false>;
+      case 2: return gemv_mfma_kernel<MODE, KH, BT, 2, true, FP8>;
+      case 3: return gemv_mfma_kernel<MODE, KH, BT, 3, true, FP8>;
+      case 4: return gemv_mfma_kernel<MODE, KH, BT, 4, true, FP8>;
+      default: return gemv_mfma_kernel<MODE, KH, BT, 2, false, FP8>;
     }
   }
 }
 
-template <int MODE, int KH>
+template <int MODE, int KH, bool FP8>
 MfmaFn pick_bt(int bt, int ups) {
-  return bt == 1 ? pick_ups<MODE, KH, 1>(ups) : pick_ups<MODE, KH, 2>(ups);
+  return bt == 1 ? pick_ups<MODE, KH, 1, FP8>(ups) : pick_ups<MODE, KH, 2, FP8>(ups);
 }
 
-template <int MODE>
+template <int MODE, bool FP8>
 MfmaFn pick_kh(int kh, int bt, int ups) {
-  return kh == 4 ? pick_bt<MODE, 4>(bt, ups) : pick_bt<MODE, 8>(bt, ups);
+  return kh == 4 ? pick_bt<MODE, 4, FP8>(bt, ups) : pick_bt<MODE, 8, FP8>(bt, ups);
+}
+
+template <bool FP8>
+MfmaFn pick_mode(GemvMode mode, int kh, int bt, int ups) {
+  switch (mode) {
+    case kGemvRmsNorm: return pick_kh<kGemvRmsNorm, FP8>(kh, bt, ups);
+    case kGemvSwiGLU: return pick_kh<kGemvSwiGLU, FP8>(kh, bt, ups);
+    case kGemvRmsNormSwiGLU: return pick_kh<kGemvRmsNormSwiGLU, FP8>(kh, bt, ups);
+    default: return pick_kh<kGemvPlain, FP8>(kh, bt, ups);
+  }
 }
 
 // Register sets: everything at once when it fits (up to 4 groups of one
@@ -310,13 +353,15 @@ bool gemv_mfma_supported(int B, int K, int N) {
 }
 
 hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
-                            const void* w0, const void* w1, void* y, int B, int K,
-                            int N, float eps, int cu_count, hipStream_t stream) {
+                            const GemvWeights& w, void* y, int B, int K, int N, float eps,
+                            int cu_count, hipStream_t stream) {
   MfmaArgs a;
   a.x = static_cast<const _Float16*>(x);
   a.gamma = static_cast<const _Float16*>(gamma);
-  a.w0 = static_cast<const _Float16*>(w0);
-  a.w1 = static_cast<const _Float16*>(w1);
+  a.w0 = w.w0;
+  a.w1 = w.w1;
+  a.s0 = w.s0;
+  a.s1 = w.s1;
   a.y = static_cast<_Float16*>(y);
   a.B = B;
   a.K = K;
@@ -331,13 +376,7 @@ hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
   const int kh = K / 512;
   const int bt = B >= 9 ? 2 : 1;  // batch column tiles of the 16-row pass
   const int ups = pick_sets(mode, a.gpw);
-  MfmaFn fn;
-  switch (mode) {
-    case kGemvRmsNorm: fn = pick_kh<kGemvRmsNorm>(kh, bt, ups); break;
-    case kGemvSwiGLU: fn = pick_kh<kGemvSwiGLU>(kh, bt, ups); break;
-    case kGemvRmsNormSwiGLU: fn = pick_kh<kGemvRmsNormSwiGLU>(kh, bt, ups); break;
-    default: fn = pick_kh<kGemvPlain>(kh, bt, ups); break;
-  }
+  const MfmaFn fn = w.fp8 ? pick_mode<true>(mode, kh, bt, ups) : pick_mode<false>(mode, kh, bt, ups);
   dim3 g(grid, (B + kBatchTile - 1) / kBatchTile);
   hipLaunchKernelGGL(fn, g, dim3(kThreadsM), 0, stream, a);
   return hipGetLastError();

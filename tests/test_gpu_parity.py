@@ -261,6 +261,9 @@ FP8_CASES = [
     ("f2n", 1, 4096, 14336), ("f2n", 5, 4096, 257),
     ("plain", 1, 14336, 4096), ("plain", 1, 4096, 4096), ("plain", 4, 14336, 512),
     ("plain", 1, 16, 5), ("plain", 12, 4096, 300),
+    # batched e4m3 on the MFMA kernel (K in {2048, 4096}, batches from 3 / 5 rows)
+    ("f1", 16, 4096, 6144), ("f1", 32, 2048, 1032), ("f2", 17, 4096, 600),
+    ("f2n", 9, 2048, 100), ("plain", 3, 2048, 8), ("plain", 16, 4096, 4100),
 ]
 
 
@@ -298,6 +301,30 @@ def test_fp8_weight_gemv_parity(mode, B, K, N):
     torch.cuda.synchronize()
     assert y.shape == (B, N)
     assert_parity(y, ref, exact, bound, f"fp8 {mode} B={B} K={K} N={N}")
+
+
+def test_fp8_mfma_and_valu_paths_agree():
+    """A batch of 8 on e4m3 weights through both kernels (the MFMA threshold
+    raised to force the VALU path) differs only by fp32 summation order."""
+    from decodebench_amd.quant import quantize_e4m3_rows
+
+    gen = torch.Generator().manual_seed(78)
+    x = randn(gen, (8, 4096)).cuda()
+    g = randn(gen, (4096,), std=0.1, mean=1.0).cuda()
+    Wq, s = (t.cuda() for t in quantize_e4m3_rows(randn(gen, (6144, 4096), std=0.02)))
+    Uq, su = (t.cuda() for t in quantize_e4m3_rows(randn(gen, (6144, 4096), std=0.02)))
+    lib = ops.load_library()
+    try:
+        outs = []
+        for thr in (2, 1 << 20):
+            assert lib.db_tune(b"gemv_mfma_min_batch", thr) == 0
+            outs.append((ops.f1_rmsnorm_gemv(x, g, Wq, w_scale=s),
+                         ops.f2_gateup_swiglu(x, Wq, Uq, s, su), ops.gemv(x, Wq, w_scale=s),
+                         ops.f2_rmsnorm_gateup_swiglu(x, g, Wq, Uq, sg=s, su=su)))
+    finally:
+        lib.db_tune(b"gemv_mfma_min_batch", 0)
+    for a, b in zip(*outs):
+        assert rel_l2(a.float().cpu().numpy(), b.float().cpu().numpy()) < 1e-3
 
 
 def test_fp8_raw_byte_weights_equal_float8_tensor():
