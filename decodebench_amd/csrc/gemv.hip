@@ -4,9 +4,9 @@
 // + SwiGLU pair of the decode-layer chain and the plain projection share one
 // kernel template (gemv_valu.h).  This file instantiates its fp16-weight half
 // and chooses the launch shape; gemv_fp8.hip instantiates the e4m3 half, and
-// batches from 3 rows (one weight matrix) or 5 rows (the gate/up pair; 4 with
-// e4m3 weights) go to the MFMA kernel (gemv_mfma.hip): the crossovers
-// measured on MI355X at K = 4096.
+// batches from 3 rows (one weight matrix) or 4 rows (the gate/up pair) go to
+// the MFMA kernel (gemv_mfma.hip): the crossovers measured on MI355X at
+// K = 4096.
 #include <mutex>
 #include <unordered_set>
 
@@ -64,7 +64,7 @@ hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
                        const GemvWeights& w, void* y, int B, int K, int N, float eps,
                        int cu_count, hipStream_t stream) {
   const int forced_min = tuning().gemv_mfma_min_batch;
-  const int mfma_min = forced_min > 0 ? forced_min : (gemv_is_swiglu(mode) ? (w.fp8 ? 4 : 5) : 3);
+  const int mfma_min = forced_min > 0 ? forced_min : (gemv_is_swiglu(mode) ? 4 : 3);
   if (B >= mfma_min && gemv_mfma_supported(B, K, N))
     return launch_gemv_mfma(mode, x, gamma, w, y, B, K, N, eps, cu_count, stream);
   GemvArgs a;

@@ -66,11 +66,9 @@ struct MfmaArgs {
 // (UPS >= groups per workgroup) they are all requested before the prologue
 // and no loop runs; otherwise two sets alternate.
 // FP8: e4m3 weights.  A 16-byte load then holds 16 weights, the A operands
-// of two k-steps after v_cvt_scalef32_pk_f16_fp8 widening: step 2p + e of
-// lane group g4 covers columns 64 p + 16 g4 + 8 e of the half slice (for
-// fp16, step t covers 32 t + 8 g4).  The activations are loaded in the same
-// column order, so the dot products are unchanged; the row scales multiply
-// the reduced sums in the epilogue.
+// of two k-steps after v_cvt_scalef32_pk_f16_fp8 widening.  The activations
+// are loaded in the same column order, so the dot products are unchanged;
+// the row scales multiply the reduced sums in the epilogue.
 template <int MODE, int KH, int BT, int UPS, bool SINGLE, bool FP8>
 __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   constexpr int NWM = gemv_is_swiglu(MODE) ? 2 : 1;
@@ -88,13 +86,18 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   const int half = c16 >> 3;  // which half of the slice this lane covers
   const int b0 = blockIdx.y * kBatchTile;
   const int nb = min(kBatchTile, a.B - b0);
-  // The slice of wave v is [v, v+1) * K / 8; this lane's half starts at sbase.
-  const int sbase = wave * KH * 64 + half * KH * 32;
-  const int kcol = sbase + 8 * g4;  // fp16: this lane's column for k-step 0
+  // The slice of wave v is [v, v+1) * K / 8.  Its columns are dealt out so
+  // that the two halves of a row are adjacent in every load instruction:
+  // fp16 k-step t covers 64 t + 32 h + 8 g4 (half h, lane group g4), e4m3
+  // load p covers 128 p + 64 h + 16 g4 (k-steps 2p and 2p + 1).  One load
+  // instruction then reads 8 full 128-byte lines, one per weight row.  The
+  // activations follow the same order; the dot products do not depend on it.
+  const int sbase = wave * KH * 64;
+  const int kcol = sbase + 32 * half + 8 * g4;  // fp16: this lane's column for k-step 0
   // Column of this lane's activation chunk for k-step t.
   auto xcol = [&](int t) {
-    if constexpr (FP8) return sbase + 64 * (t >> 1) + 16 * g4 + 8 * (t & 1);
-    return kcol + 32 * t;
+    if constexpr (FP8) return sbase + 128 * (t >> 1) + 64 * half + 16 * g4 + 8 * (t & 1);
+    return kcol + 64 * t;
   };
 
   // ---- activation slice -> registers (B operand), loads unconditional ----
@@ -108,7 +111,7 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
     const int xrow = b0 + min(8 * bt + r8, nb - 1);
 #pragma unroll
     for (int t = 0; t < KH; ++t)
-      xr[bt][t] = ld16(a.x + (size_t)xrow * a.K + (FP8 ? xcol(t) : kcol + 32 * t));
+      xr[bt][t] = ld16(a.x + (size_t)xrow * a.K + (FP8 ? xcol(t) : kcol + 64 * t));
   }
   u4 gchunk = {0, 0, 0, 0};
   if constexpr (gemv_has_norm(MODE))
@@ -135,7 +138,7 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
           dst[q][m][t] =
               FP8 ? ld_stream(wmat[m] + (size_t)row * a.K + xcol(2 * t))
                   : ld_stream(reinterpret_cast<const _Float16*>(wmat[m]) + (size_t)row * a.K +
-                              kcol + 32 * t);
+                              kcol + 64 * t);
     }
   };
 
@@ -181,7 +184,7 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
       const float inv = 1.0f / sqrtf(tot / (float)a.K + a.eps);
 #pragma unroll
       for (int t = 0; t < KH; ++t) {
-        const u4 gv = s_gamma[(FP8 ? xcol(t) : kcol + 32 * t) / 8];
+        const u4 gv = s_gamma[(FP8 ? xcol(t) : kcol + 64 * t) / 8];
         u4 out;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
