@@ -190,7 +190,11 @@ PROFILE_WORKLOADS = (("f1_cfg1", dict(name="f1")), ("f1_qkv_cfg3", dict(name="f1
                      ("f1_qkv_cfg3_fp8", dict(name="f1_qkv", dtype="fp8")),
                      ("f2_cfg2_fp8", dict(name="f2", dtype="fp8")),
                      ("layer_cfg5", dict(name="layer", L=8192)),
-                     ("layer_cfg5_fp8", dict(name="layer", L=8192, dtype="fp8")))
+                     ("layer_cfg5_fp8", dict(name="layer", L=8192, dtype="fp8")),
+                     ("f1_qkv_cfg3_B16", dict(name="f1_qkv", batch=16)),
+                     ("f1_qkv_cfg3_B32", dict(name="f1_qkv", batch=32)),
+                     ("f2_cfg2_B16", dict(name="f2", batch=16)),
+                     ("f2_cfg2_fp8_B16", dict(name="f2", batch=16, dtype="fp8")))
 
 
 def kernels_per_call(kw: dict) -> int:
@@ -228,7 +232,7 @@ def profile_pass(manifest_path: str, calls: int = 24, warmup: int = 4) -> int:
     del src, dst
     workloads = []
     for label, kw in PROFILE_WORKLOADS:
-        case = build_config(batch=1, gen_device="cuda", **kw)
+        case = build_config(gen_device="cuda", **{"batch": 1, **kw})
         per_call = kernels_per_call(kw)
         n = len(case.replicas)
         for i in range(calls):
