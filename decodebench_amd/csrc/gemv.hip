@@ -45,8 +45,8 @@ int pick_waves(int groups, int cu_count) {
   return waves_for(groups, cu_count * (forced > 0 ? forced : 32));
 }
 
-// Raise a kernel's dynamic-LDS limit to the 152 KB activation budget, once
-// per kernel function (the attribute is per function, not per launch).
+}  // namespace
+
 hipError_t allow_large_lds(const void* fn) {
   static std::mutex mu;
   static std::unordered_set<const void*> done;
@@ -57,8 +57,6 @@ hipError_t allow_large_lds(const void* fn) {
   if (e == hipSuccess) done.insert(fn);
   return e;
 }
-
-}  // namespace
 
 hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
                        const GemvWeights& w, void* y, int B, int K, int N, float eps,

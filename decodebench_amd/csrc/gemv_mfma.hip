@@ -44,7 +44,9 @@ constexpr int kWavesM = 8;
 constexpr int kThreadsM = kWavesM * kWave;
 constexpr int kRowsPerGroup = 8;
 constexpr int kBatchTile = 16;
-constexpr int kMaxGroupsPerWg = 8;   // LDS partial-sum slots per workgroup
+// Groups per workgroup: 16 keeps the gate/up pair of N = 14336 (3584
+// groups) on one workgroup per CU, 14 groups each.
+constexpr int kMaxGroupsPerWg = 16;
 
 struct MfmaArgs {
   const _Float16* x;      // [B, K]
@@ -73,8 +75,12 @@ template <int MODE, int KH, int BT, int UPS, bool SINGLE, bool FP8>
 __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   constexpr int NWM = gemv_is_swiglu(MODE) ? 2 : 1;
   constexpr int KW = FP8 ? KH / 2 : KH;  // 16-byte weight loads per row and slice
-  // [group][matrix][wave][batch][row]
-  __shared__ __align__(16) float part[kMaxGroupsPerWg][NWM][kWavesM][kBatchTile][kRowsPerGroup];
+  // Dynamic LDS, [group < gpw][matrix][wave][batch < 8 BT][row]: the 8
+  // K-slice partial sums of every output of the workgroup.
+  extern __shared__ __align__(16) float part[];
+  auto slot = [&](int j, int m, int v, int n) -> float* {
+    return part + ((((j * NWM + m) * kWavesM + v) * (8 * BT) + n) * kRowsPerGroup);
+  };
   __shared__ float red[kWavesM][kBatchTile];
   __shared__ u4 s_gamma[gemv_has_norm(MODE) ? kThreadsM : 1];  // K / 8 chunks
 
@@ -102,9 +108,7 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
 
   // ---- activation slice -> registers (B operand), loads unconditional ----
   // F1's gamma is shared by every batch row: thread t fetches 16-byte chunk t
-  // (K / 8 <= 512 chunks) for the LDS copy the normalisation reads.  Both
-  // are issued before the first weight loads, so waiting for them never
-  // waits for weights (loads complete in issue order).
+  // (K / 8 <= 512 chunks) for the LDS copy the normalisation reads.
   u4 xr[BT][KH];
 #pragma unroll
   for (int bt = 0; bt < BT; ++bt) {
@@ -142,10 +146,13 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
     }
   };
 
-  u4 wa[UPS][NWM][KW];
-  load_set(wa, 0, true);  // every workgroup owns at least one group
-  __builtin_amdgcn_sched_barrier(0);
-
+  // x is read by every workgroup (B x K x 2 bytes per CU).  On MI355X its
+  // arrival, 1-2 us at batch 4 and 3-5 us at batch 16 with no weight
+  // traffic, stretches to 5-20 us when it queues behind the weights the
+  // other workgroups have requested.  With one batch tile the wave waits
+  // for its slice before requesting weights (batch 3-8 runs 0.4-1.3 us
+  // faster); with two tiles waiting costs more than it saves, and set A is
+  // requested first.
   const u4 zero4 = {0, 0, 0, 0};
 #pragma unroll
   for (int bt = 0; bt < BT; ++bt) {
@@ -153,6 +160,15 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
 #pragma unroll
     for (int t = 0; t < KH; ++t) xr[bt][t] = valid ? xr[bt][t] : zero4;
   }
+  if constexpr (BT == 1) {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x and gamma are here
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  u4 wa[UPS][NWM][KW];
+  load_set(wa, 0, true);  // every workgroup owns at least one group
+  __builtin_amdgcn_sched_barrier(0);
 
   if constexpr (gemv_has_norm(MODE)) {
     // x^2 over this slice per batch row: in-lane, then over the two halves
@@ -229,7 +245,7 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[i] += __shfl(acc[i], lane + 40);
           if (g4 < 2 && c16 < 8)
-            *reinterpret_cast<f4*>(&part[j][m][wave][8 * bt + c16][4 * g4]) = acc;
+            *reinterpret_cast<f4*>(slot(j, m, wave, 8 * bt + c16) + 4 * g4) = acc;
         }
       }
     }
@@ -260,18 +276,18 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   __syncthreads();
 
   // ---- reduce the 8 K-slices, epilogue, fp16 store ----------------------
-  const int nout = my_groups * kBatchTile * kRowsPerGroup;
+  const int nout = my_groups * 8 * BT * kRowsPerGroup;
   for (int idx = threadIdx.x; idx < nout; idx += kThreadsM) {
-    const int jj = idx / (kBatchTile * kRowsPerGroup);
-    const int n = (idx / kRowsPerGroup) % kBatchTile;
+    const int jj = idx / (8 * BT * kRowsPerGroup);
+    const int n = (idx / kRowsPerGroup) % (8 * BT);
     const int r = idx % kRowsPerGroup;
     const int row = (blockIdx.x + gridDim.x * jj) * kRowsPerGroup + r;
     if (n >= nb || row >= a.N) continue;
     float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
     for (int v = 0; v < kWavesM; ++v) {
-      s0 += part[jj][0][v][n][r];
-      if constexpr (NWM == 2) s1 += part[jj][NWM - 1][v][n][r];
+      s0 += slot(jj, 0, v, n)[r];
+      if constexpr (NWM == 2) s1 += slot(jj, NWM - 1, v, n)[r];
     }
     if constexpr (FP8) {
       s0 *= a.s0[row];
@@ -380,8 +396,14 @@ hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
   const int bt = B >= 9 ? 2 : 1;  // batch column tiles of the 16-row pass
   const int ups = pick_sets(mode, a.gpw);
   const MfmaFn fn = w.fp8 ? pick_mode<true>(mode, kh, bt, ups) : pick_mode<false>(mode, kh, bt, ups);
+  const int nwm = gemv_is_swiglu(mode) ? 2 : 1;
+  const size_t lds = sizeof(float) * a.gpw * nwm * kWavesM * 8 * bt * kRowsPerGroup;
+  if (lds > 48 * 1024) {
+    hipError_t e = allow_large_lds(reinterpret_cast<const void*>(fn));
+    if (e != hipSuccess) return e;
+  }
   dim3 g(grid, (B + kBatchTile - 1) / kBatchTile);
-  hipLaunchKernelGGL(fn, g, dim3(kThreadsM), 0, stream, a);
+  hipLaunchKernelGGL(fn, g, dim3(kThreadsM), lds, stream, a);
   return hipGetLastError();
 }
 

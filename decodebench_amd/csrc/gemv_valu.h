@@ -62,6 +62,10 @@ using GemvFn = void (*)(GemvArgs);
 GemvFn gemv_pick_f16(GemvMode mode, int nb, int u);
 GemvFn gemv_pick_fp8(GemvMode mode, int nb, int u);
 
+// Raise a kernel's dynamic-LDS limit to 152 KB, once per kernel function
+// (the attribute is per function, not per launch).  Defined in gemv.hip.
+hipError_t allow_large_lds(const void* fn);
+
 // Rows per wave group, measured on MI355X at the decode shapes: fp16 keeps
 // 16 loads of 16 bytes per lane per tile (2 rows x 8 chunks, or the gate/up
 // pair x 1 row); e4m3 rows are half as long, and 2 rows per group (8 loads
