@@ -4,9 +4,8 @@
 // + SwiGLU pair of the decode-layer chain and the plain projection share one
 // kernel template (gemv_valu.h).  This file instantiates its fp16-weight half
 // and chooses the launch shape; gemv_fp8.hip instantiates the e4m3 half, and
-// batches from 3 rows (one weight matrix) or 4 rows (the gate/up pair) go to
-// the MFMA kernel (gemv_mfma.hip): the crossovers measured on MI355X at
-// K = 4096.
+// batches from 3 rows (2 for the e4m3 gate/up pair) go to the MFMA kernel
+// (gemv_mfma.hip): the crossovers measured on MI355X at K = 4096.
 #include <mutex>
 #include <unordered_set>
 
@@ -62,7 +61,11 @@ hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
                        const GemvWeights& w, void* y, int B, int K, int N, float eps,
                        int cu_count, hipStream_t stream) {
   const int forced_min = tuning().gemv_mfma_min_batch;
-  const int mfma_min = forced_min > 0 ? forced_min : (gemv_is_swiglu(mode) ? 4 : 3);
+  // Measured at K = 4096 (graph back-to-back): the VALU kernel wins at 2
+  // rows except for the e4m3 gate/up pair (22.4 vs 19.2 us); at 3 rows it
+  // would run two 2-row passes, 1.5-1.8x the MFMA time.
+  const int auto_min = gemv_is_swiglu(mode) && w.fp8 ? 2 : 3;
+  const int mfma_min = forced_min > 0 ? forced_min : auto_min;
   if (B >= mfma_min && gemv_mfma_supported(B, K, N))
     return launch_gemv_mfma(mode, x, gamma, w, y, B, K, N, eps, cu_count, stream);
   GemvArgs a;

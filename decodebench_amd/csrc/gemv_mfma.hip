@@ -93,17 +93,19 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   const int half = c16 >> 3;  // which half of the slice this lane covers
   const int b0 = blockIdx.y * kBatchTile;
   const int nb = min(kBatchTile, a.B - b0);
-  // Wave v of workgroup w owns slice s = (v + w) mod 8, columns
-  // [s, s+1) * K / 8: neighbouring workgroups start on different slices, so
-  // the L2 channels serving x see the 256 copies of it spread over its whole
-  // extent (x arrives 1.5x sooner at batch 16; e4m3 batches 4-8% faster).
+  // Wave v of workgroup w owns slice s = (v + w + w / 8) mod 8, columns
+  // [s, s+1) * K / 8: workgroups on one XCD (w, w + 8, ...) and on
+  // neighbouring XCDs start on different slices, so the 256 reads of x are
+  // spread over its whole extent (x arrives 1.5x sooner at batch 16 than
+  // with one order everywhere; e4m3 batches 4-8% faster).
   // The slice's columns are dealt out so that the two halves of a row are
   // adjacent in every load instruction:
   // fp16 k-step t covers 64 t + 32 h + 8 g4 (half h, lane group g4), e4m3
   // load p covers 128 p + 64 h + 16 g4 (k-steps 2p and 2p + 1).  One load
   // instruction then reads 8 full 128-byte lines, one per weight row.  The
   // activations follow the same order; the dot products do not depend on it.
-  const int sbase = ((wave + (int)blockIdx.x) & (kWavesM - 1)) * KH * 64;
+  const int sbase =
+      ((wave + (int)blockIdx.x + ((int)blockIdx.x >> 3)) & (kWavesM - 1)) * KH * 64;
   const int kcol = sbase + 32 * half + 8 * g4;  // fp16: this lane's column for k-step 0
   // Column of this lane's activation chunk for k-step t.
   auto xcol = [&](int t) {

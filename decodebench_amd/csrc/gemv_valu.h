@@ -152,11 +152,20 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
   // (clamped addresses, masked afterwards) and their uses straight-line, so
   // the compiler waits for them alone and not for the weights.
   constexpr int kPre = 2;  // covers K <= 2 * 256 * 8 = 4096 with no reload
+  static_assert((kPre * kThreads & (kPre * kThreads - 1)) == 0, "slot count: power of 2");
+  // Pass i of thread t fills chunk pre_chunk(i), a permutation of the
+  // kPre * kThreads slots rotated by 1 KB per workgroup: workgroups on one
+  // XCD (w, w + 8, ...) and on neighbouring XCDs start on different parts
+  // of x, which every workgroup reads.
+  const int rot = 64 * (((int)blockIdx.x + ((int)blockIdx.x >> 3)) & 7);
+  auto pre_chunk = [&](int i) {
+    return ((int)threadIdx.x + i * kThreads + rot) & (kPre * kThreads - 1);
+  };
   u4 xr[kPre][NB];
   u4 gr[kPre];
 #pragma unroll
   for (int i = 0; i < kPre; ++i) {
-    const int c = min((int)threadIdx.x + i * kThreads, a.kchunks - 1);
+    const int c = min(pre_chunk(i), a.kchunks - 1);
     gr[i] = u4{0, 0, 0, 0};
     if constexpr (kNorm) gr[i] = ld16(a.gamma + (size_t)c * 8);
 #pragma unroll
@@ -180,7 +189,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
   const u4 zero4 = {0, 0, 0, 0};
 #pragma unroll
   for (int i = 0; i < kPre; ++i) {
-    const bool valid_c = (int)threadIdx.x + i * kThreads < a.kchunks;
+    const bool valid_c = pre_chunk(i) < a.kchunks;
     gr[i] = valid_c ? gr[i] : zero4;
 #pragma unroll
     for (int b = 0; b < NB; ++b) xr[i][b] = (valid_c && b < nb) ? xr[i][b] : zero4;
@@ -240,7 +249,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
     };
 #pragma unroll
     for (int i = 0; i < kPre; ++i) {
-      const int c = threadIdx.x + i * kThreads;
+      const int c = pre_chunk(i);
       if (c < a.kp8)
 #pragma unroll
         for (int b = 0; b < NB; ++b) xs[b * a.kp8 + c] = norm(xr[i][b], gr[i], inv[b]);
@@ -253,7 +262,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
   } else {
 #pragma unroll
     for (int i = 0; i < kPre; ++i) {
-      const int c = threadIdx.x + i * kThreads;
+      const int c = pre_chunk(i);
       if (c < a.kp8)
 #pragma unroll
         for (int b = 0; b < NB; ++b) xs[b * a.kp8 + c] = xr[i][b];

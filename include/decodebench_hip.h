@@ -145,8 +145,8 @@ int db_f4_splitkv(const void* q, const void* k, const void* v, void* o,
 int db_null_kernel(void* stream);
 
 /* Launch-geometry knobs for tuning sweeps: "gemv_waves_per_cu" (<= 0: the
- * default, 32), "gemv_mfma_min_batch" (0: automatic, 3 for one weight matrix
- * and 4 for the gate/up pair), "f4_blocks_per_cu", "f4_min_tiles",
+ * default, 32), "gemv_mfma_min_batch" (0: automatic, 3 rows, 2 for the
+ * e4m3 gate/up pair), "f4_blocks_per_cu", "f4_min_tiles",
  * "f4_waves" (4 or 8 waves per workgroup, 0: automatic) and "f4_merge" (0: the
  * split merge runs in a second launch, the default; 1: in the same launch).
  * Process-wide; no counterpart in the reference. */

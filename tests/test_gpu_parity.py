@@ -124,13 +124,14 @@ def test_plain_gemv_parity():
 
 
 # --------------------------------------------------- batched GEMV (MFMA)
-# Batches from 3 rows (one weight matrix) or 4 rows (gate/up pair) with K in
+# Batches from 3 rows (2 for the e4m3 gate/up pair) with K in
 # {2048, 4096} take the MFMA kernel: ragged batches (one and two 16-row
 # passes), N not a multiple of the 8-row group.
 MFMA_CASES = [
     ("f1", 3, 4096, 1000), ("f1", 17, 4096, 6144), ("f1", 32, 2048, 1032),
     ("f2", 4, 4096, 14336), ("f2", 32, 4096, 1792), ("f2", 9, 2048, 777),
-    ("plain", 16, 4096, 4100), ("plain", 3, 2048, 8),
+    ("plain", 16, 4096, 4100), ("plain", 3, 2048, 8), ("f2", 3, 4096, 1000),
+    ("f2", 3, 2048, 515),
 ]
 
 
@@ -261,9 +262,10 @@ FP8_CASES = [
     ("f2n", 1, 4096, 14336), ("f2n", 5, 4096, 257),
     ("plain", 1, 14336, 4096), ("plain", 1, 4096, 4096), ("plain", 4, 14336, 512),
     ("plain", 1, 16, 5), ("plain", 12, 4096, 300),
-    # batched e4m3 on the MFMA kernel (K in {2048, 4096}, batches from 3 / 4 rows)
+    # batched e4m3 on the MFMA kernel (K in {2048, 4096}, batches from 2 / 3 rows)
     ("f1", 16, 4096, 6144), ("f1", 32, 2048, 1032), ("f2", 17, 4096, 600),
     ("f2n", 9, 2048, 100), ("plain", 3, 2048, 8), ("plain", 16, 4096, 4100),
+    ("f2", 2, 4096, 520), ("f2n", 2, 4096, 1000),
 ]
 
 
