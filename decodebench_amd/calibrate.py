@@ -20,6 +20,13 @@ The counterpart of the reference's ``calibrate`` harness
 
 The printed lines follow calibrate.cu's output ("t_launch_stream: ... us",
 "G2: PASS"), with the vendor line labelled by the library that ran.
+
+One comparison has no counterpart in the reference: :func:`vendor_f4` times
+F4 (``db_f4_splitkv``) against torch's ``scaled_dot_product_attention`` at
+the BASELINE decode shape (32 query heads, 8 KV heads, head dim 128, fp16,
+Q/K/V ~ N(0, 1)), both replayed back to back in a hipGraph over
+cache-defeating KV replicas, and reports their largest output difference as
+an independent cross-check of F4's results.
 """
 
 from __future__ import annotations
@@ -66,6 +73,92 @@ class GateG2:
                 f"  {self.vendor}: {self.us_vendor:.2f} us  ({self.gbs_vendor:.2f} GB/s)\n"
                 f"  Ratio (ours/{self.vendor}): {self.ratio * 100.0:.1f}%\n"
                 f"G2: {'PASS' if self.passed else 'FAIL'}")
+
+
+@dataclass
+class VendorF4:
+    B: int
+    L: int
+    us_ours: float
+    us_vendor: float
+    replicas: int
+    max_abs_diff: float
+
+    @property
+    def speedup(self) -> float:
+        return self.us_vendor / self.us_ours
+
+    def render(self) -> str:
+        return (f"F4 attention B={self.B} Hq=32 Hkv=8 D=128 L={self.L} ({self.replicas} KV "
+                f"replica{'s' if self.replicas != 1 else ''})\n"
+                f"  Ours (db_f4_splitkv): {self.us_ours:.2f} us\n"
+                f"  torch SDPA:           {self.us_vendor:.2f} us\n"
+                f"  Speed-up (SDPA / ours): {self.speedup:.2f}x\n"
+                f"  max |ours - SDPA|: {self.max_abs_diff:.3e}")
+
+
+def _graph_us(fn, args: list, min_launches: int = 48, replays: int = 10) -> float:
+    """Median per-call microseconds of ``fn(args[i])`` replayed back to back
+    in one hipGraph that cycles through ``args``."""
+    import torch
+
+    n = len(args)
+    per_graph = n * max(1, -(-min_launches // n))
+    for a in args:  # first calls allocate (workspaces) outside the capture
+        fn(a)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for a in args:
+            fn(a)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(per_graph):
+            fn(args[i % n])
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = _events()
+    samples = []
+    for _ in range(replays):
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        samples.append(e0.elapsed_time(e1) * 1e3 / per_graph)
+    del graph
+    samples.sort()
+    return samples[len(samples) // 2]
+
+
+def vendor_f4(L: int = 8192, B: int = 1, seed: int = 42) -> VendorF4:
+    import torch
+    import torch.nn.functional as F
+
+    from decodebench_amd import ops
+    from decodebench_amd.timing import cache_defeat_replicas
+
+    ops.load_library()
+    Hq, Hkv, D = 32, 8, 128
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=gen, device="cuda", dtype=torch.float32).half()
+
+    q = randn(B, Hq, D)
+    n = cache_defeat_replicas(2 * B * Hkv * L * D * 2)
+    kv = [(randn(B, Hkv, L, D), randn(B, Hkv, L, D)) for _ in range(n)]
+    q4 = q.view(B, Hq, 1, D)
+
+    def ours(r):
+        return ops.f4_flashdecode(q, r[0], r[1])
+
+    def sdpa(r):
+        return F.scaled_dot_product_attention(q4, r[0], r[1], enable_gqa=True)
+
+    diff = float((ours(kv[0]).float() - sdpa(kv[0]).view(B, Hq, D).float()).abs().max())
+    return VendorF4(B, L, _graph_us(ours, kv), _graph_us(sdpa, kv), n, diff)
 
 
 def _events():

@@ -16,7 +16,8 @@ Two additions for this build:
   ``Sequence.profile``, so the report adds the fused time and its residual;
 * ``calibrate --null | --gate-g2`` is the calibration harness
   (validation/src/bench/calibrate.cu:42-230, see
-  ``decodebench_amd.calibrate``).
+  ``decodebench_amd.calibrate``); ``calibrate --vendor-f4`` adds F4 against
+  torch's scaled_dot_product_attention.
 
 The GPU is only touched after argument validation and dry runs.
 """
@@ -88,6 +89,10 @@ def build_parser() -> argparse.ArgumentParser:
                        help="Launches per measurement (default 500 null, 200 GEMV).")
     cal_p.add_argument("--no-rotate", action="store_true",
                        help="G2 on one weight matrix, as the reference (cache-resident here).")
+    cal_p.add_argument("--vendor-f4", action="store_true",
+                       help="Compare F4 with torch scaled_dot_product_attention.")
+    cal_p.add_argument("--kv-len", type=int, default=8192, help="KV length for --vendor-f4.")
+    cal_p.add_argument("--kv-batch", type=int, default=1, help="Batch for --vendor-f4.")
     cal_p.add_argument("--dry-run", action="store_true", help="Print plan and exit.")
     return parser
 
@@ -202,16 +207,21 @@ def _sweep(args) -> int:
 
 
 def _calibrate(args) -> int:
-    if not (args.null or args.gate_g2):
-        print("Error: calibrate needs --null and/or --gate-g2", file=sys.stderr)
+    if not (args.null or args.gate_g2 or args.vendor_f4):
+        print("Error: calibrate needs --null, --gate-g2 and/or --vendor-f4", file=sys.stderr)
         return 2
     if args.iters is not None and args.iters < 1:
         print("Error: --iters must be >= 1", file=sys.stderr)
         return 2
+    if args.kv_len < 1 or args.kv_batch < 1:
+        print("Error: --kv-len and --kv-batch must be >= 1", file=sys.stderr)
+        return 2
     if args.dry_run:
-        what = [w for w, on in (("null", args.null), ("gate-g2", args.gate_g2)) if on]
+        what = [w for w, on in (("null", args.null), ("gate-g2", args.gate_g2),
+                                ("vendor-f4", args.vendor_f4)) if on]
         print(f"[dry-run] calibrate {' '.join(what)} with iters={args.iters or 'default'}, "
-              f"rotate={not args.no_rotate}")
+              f"rotate={not args.no_rotate}"
+              + (f", kv_len={args.kv_len}, kv_batch={args.kv_batch}" if args.vendor_f4 else ""))
         return 0
     if not _gpu_or_error():
         return 1
@@ -225,6 +235,13 @@ def _calibrate(args) -> int:
         print(g2.render())
         if g2.max_abs_diff > 5e-2:
             print(f"Error: GEMV output differs from the vendor BLAS by {g2.max_abs_diff:.3e}",
+                  file=sys.stderr)
+            rc = 1
+    if args.vendor_f4:
+        v = calibrate.vendor_f4(L=args.kv_len, B=args.kv_batch)
+        print(v.render())
+        if v.max_abs_diff > 5e-3:
+            print(f"Error: F4 output differs from torch SDPA by {v.max_abs_diff:.3e}",
                   file=sys.stderr)
             rc = 1
     return rc

@@ -60,6 +60,10 @@ def test_cli_calibrate_validation(capsys):
     assert main(["calibrate", "--null", "--iters", "0"]) == 2
     assert main(["calibrate", "--null", "--gate-g2", "--dry-run"]) == 0
     assert "[dry-run] calibrate null gate-g2" in capsys.readouterr()[0]
+    assert main(["calibrate", "--vendor-f4", "--kv-len", "0"]) == 2
+    assert main(["calibrate", "--vendor-f4", "--kv-len", "1024", "--dry-run"]) == 0
+    assert "vendor-f4 with iters=default, rotate=True, kv_len=1024, kv_batch=1" in \
+        capsys.readouterr()[0]
 
 
 def test_sweep_csv_header_matches_the_reference():
@@ -76,6 +80,16 @@ def test_cli_calibrate_on_gpu(capsys):
                  "GEMV d_out=14336 d_in=4096", "Ratio (ours/"):
         assert line in out
     assert "G2: PASS" in out or "G2: FAIL" in out
+
+
+@pytest.mark.gpu
+def test_cli_calibrate_vendor_f4(capsys):
+    # F4 against torch SDPA at L=1024: also an independent check of F4's output.
+    assert main(["calibrate", "--vendor-f4", "--kv-len", "1024", "--kv-batch", "2"]) == 0
+    out = capsys.readouterr()[0]
+    for line in ("F4 attention B=2 Hq=32 Hkv=8 D=128 L=1024", "Ours (db_f4_splitkv):",
+                 "torch SDPA:", "max |ours - SDPA|:"):
+        assert line in out
 
 
 @pytest.mark.gpu
