@@ -82,10 +82,17 @@ hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
   a.eps = eps;
   a.kchunks = K / 8;
   a.wchunks = w.fp8 ? K / 16 : K / 8;
-  const int U = pick_chunks_per_lane(a.wchunks);
+  // Activation chunks one k-step spans (two per weight chunk for fp8); the
+  // row is padded to whole k-steps.  Near the LDS budget a masked 8-chunk
+  // step can pad an e4m3 row past it (K = 77808: 4863 weight chunks pad to
+  // 5120, 160 KB of activations); fewer chunks per lane pad less.
+  int U = pick_chunks_per_lane(a.wchunks);
+  auto padded_chunks = [&](int u) {
+    return (a.wchunks + kWave * u - 1) / (kWave * u) * kWave * u * (w.fp8 ? 2 : 1);
+  };
+  while (U > 1 && (size_t)padded_chunks(U) * 16 > 152 * 1024) U = U >= 7 ? 4 : U / 2;
   a.steps = (a.wchunks + kWave * U - 1) / (kWave * U);
-  // Activation chunks one k-step spans (two per weight chunk for fp8).
-  a.kp8 = a.steps * kWave * U * (w.fp8 ? 2 : 1);
+  a.kp8 = padded_chunks(U);
   const int R = gemv_rows_per_group(mode, w.fp8, U);
   a.groups = (N + R - 1) / R;
 

@@ -188,7 +188,9 @@ def test_mfma_and_valu_gemv_paths_agree():
 # budget), for fp16 and e4m3 weights.
 EDGE_CASES = [("f1", 1, 8, 1, "f16"), ("plain", 3, 8, 5, "f16"), ("f2", 2, 16, 1, "f16"),
               ("f1", 1, 77824, 64, "f16"), ("plain", 1, 77824, 33, "fp8"),
-              ("f2", 1, 77824, 17, "fp8"), ("plain", 1, 16, 1, "fp8")]
+              ("f2", 1, 77824, 17, "fp8"), ("plain", 1, 16, 1, "fp8"),
+              # e4m3 row whose 8-chunk k-steps would pad past the LDS budget
+              ("plain", 1, 77808, 9, "fp8"), ("f2", 2, 77808, 5, "fp8")]
 
 
 @pytest.mark.parametrize("mode,B,K,N,dtype", EDGE_CASES)
