@@ -17,6 +17,7 @@ ops raise ``RuntimeError`` naming the build command.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes as C
 import math
 import threading
@@ -110,6 +111,25 @@ def _require(t, name: str, dtype=None) -> None:
         raise ValueError(f"{name} must be contiguous")
 
 
+def _same_device(*named) -> None:
+    """All tensors of one call must live on one GPU."""
+    dev = named[0][0].device
+    for t, name in named[1:]:
+        if t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, expected {dev} like {named[0][1]}")
+
+
+def _on_device(t):
+    """Make t's GPU current for the library call (its launches and CU-count
+    query use the current HIP device); a no-op when it already is."""
+    import torch
+
+    idx = t.device.index
+    if idx is None or idx == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(idx)
+
+
 def cu_count(device=None) -> int:
     import torch
 
@@ -126,8 +146,9 @@ def null_kernel(device=None) -> None:
     import torch
 
     dev = torch.device("cuda" if device is None else device)
-    _check(load_library().db_null_kernel(torch.cuda.current_stream(dev).cuda_stream),
-           "db_null_kernel")
+    with torch.cuda.device(dev):
+        rc = load_library().db_null_kernel(torch.cuda.current_stream(dev).cuda_stream)
+    _check(rc, "db_null_kernel")
 
 
 def tune(key: str, value: int) -> None:
@@ -178,10 +199,12 @@ def f1_rmsnorm_gemv(x, g, W, eps: float = 1e-6, w_scale=None):
                          f"W {tuple(W.shape)}")
     N = W.shape[0]
     dt, sp = _weights(W, w_scale, "W", N, K)
+    _same_device((x, "x"), (g, "g"), (W, "W"), *(((w_scale, "w_scale"),) if sp else ()))
     y = torch.empty((B, N), dtype=torch.float16, device=x.device)
-    rc = load_library().db_f1_rmsnorm_gemv(x2.data_ptr(), g.data_ptr(), W.data_ptr(), sp,
-                                           y.data_ptr(), B, K, N, float(eps), dt,
-                                           _stream_ptr(x))
+    with _on_device(x):
+        rc = load_library().db_f1_rmsnorm_gemv(x2.data_ptr(), g.data_ptr(), W.data_ptr(), sp,
+                                               y.data_ptr(), B, K, N, float(eps), dt,
+                                               _stream_ptr(x))
     _check(rc, "db_f1_rmsnorm_gemv")
     return y[0] if squeeze else y
 
@@ -203,10 +226,13 @@ def f2_gateup_swiglu(x, Wg, Wu, sg=None, su=None):
     N = Wg.shape[0]
     dt, sgp = _weights(Wg, sg, "Wg", N, K)
     _, sup = _weights(Wu, su, "Wu", N, K)
+    _same_device((x, "x"), (Wg, "Wg"), (Wu, "Wu"),
+                 *(((sg, "sg"), (su, "su")) if sgp else ()))
     y = torch.empty((B, N), dtype=torch.float16, device=x.device)
-    rc = load_library().db_f2_gateup_swiglu(x2.data_ptr(), Wg.data_ptr(), Wu.data_ptr(),
-                                            sgp, sup, y.data_ptr(), B, K, N, dt,
-                                            _stream_ptr(x))
+    with _on_device(x):
+        rc = load_library().db_f2_gateup_swiglu(x2.data_ptr(), Wg.data_ptr(), Wu.data_ptr(),
+                                                sgp, sup, y.data_ptr(), B, K, N, dt,
+                                                _stream_ptr(x))
     _check(rc, "db_f2_gateup_swiglu")
     return y[0] if squeeze else y
 
@@ -233,10 +259,13 @@ def f2_rmsnorm_gateup_swiglu(x, g, Wg, Wu, eps: float = 1e-6, sg=None, su=None):
     N = Wg.shape[0]
     dt, sgp = _weights(Wg, sg, "Wg", N, K)
     _, sup = _weights(Wu, su, "Wu", N, K)
+    _same_device((x, "x"), (g, "g"), (Wg, "Wg"), (Wu, "Wu"),
+                 *(((sg, "sg"), (su, "su")) if sgp else ()))
     y = torch.empty((B, N), dtype=torch.float16, device=x.device)
-    rc = load_library().db_f2_rmsnorm_gateup_swiglu(
-        x2.data_ptr(), g.data_ptr(), Wg.data_ptr(), Wu.data_ptr(), sgp, sup, y.data_ptr(),
-        B, K, N, float(eps), dt, _stream_ptr(x))
+    with _on_device(x):
+        rc = load_library().db_f2_rmsnorm_gateup_swiglu(
+            x2.data_ptr(), g.data_ptr(), Wg.data_ptr(), Wu.data_ptr(), sgp, sup, y.data_ptr(),
+            B, K, N, float(eps), dt, _stream_ptr(x))
     _check(rc, "db_f2_rmsnorm_gateup_swiglu")
     return y[0] if squeeze else y
 
@@ -253,9 +282,11 @@ def gemv(x, W, w_scale=None):
         raise ValueError(f"shape mismatch: x {tuple(x.shape)}, W {tuple(W.shape)}")
     N = W.shape[0]
     dt, sp = _weights(W, w_scale, "W", N, K)
+    _same_device((x, "x"), (W, "W"), *(((w_scale, "w_scale"),) if sp else ()))
     y = torch.empty((B, N), dtype=torch.float16, device=x.device)
-    rc = load_library().db_gemv(x2.data_ptr(), W.data_ptr(), sp, y.data_ptr(), B, K, N, dt,
-                                _stream_ptr(x))
+    with _on_device(x):
+        rc = load_library().db_gemv(x2.data_ptr(), W.data_ptr(), sp, y.data_ptr(), B, K, N, dt,
+                                    _stream_ptr(x))
     _check(rc, "db_gemv")
     return y[0] if squeeze else y
 
@@ -303,6 +334,8 @@ def f4_flashdecode(q, K, V, scale: float | None = None, n_splits: int | None = N
     Bk, Hkv, L, Dk = K.shape
     if Bk != B or Dk != D:
         raise ValueError(f"q {tuple(q.shape)} and K {tuple(K.shape)} disagree on B or D")
+    _same_device((q, "q"), (K, "K"), (V, "V"),
+                 *(((workspace, "workspace"),) if workspace is not None else ()))
     scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
     S = f4_default_splits(B, Hkv, L, q.device) if n_splits is None else int(n_splits)
     if workspace is None:
@@ -310,8 +343,9 @@ def f4_flashdecode(q, K, V, scale: float | None = None, n_splits: int | None = N
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     o = torch.empty((B, Hq, D), dtype=torch.float16, device=q.device)
-    rc = load_library().db_f4_splitkv(q.data_ptr(), K.data_ptr(), V.data_ptr(), o.data_ptr(),
-                                      ws_ptr, ws_bytes, B, Hq, Hkv, L, D, S, scale,
-                                      _stream_ptr(q))
+    with _on_device(q):
+        rc = load_library().db_f4_splitkv(q.data_ptr(), K.data_ptr(), V.data_ptr(), o.data_ptr(),
+                                          ws_ptr, ws_bytes, B, Hq, Hkv, L, D, S, scale,
+                                          _stream_ptr(q))
     _check(rc, "db_f4_splitkv")
     return o

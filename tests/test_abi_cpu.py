@@ -169,3 +169,13 @@ def test_python_wrappers_raise_on_cpu_tensors():
     with pytest.raises(ValueError, match="GPU"):
         ops.f1_rmsnorm_gemv(x, torch.zeros(64, dtype=torch.float16),
                             torch.zeros(8, 64, dtype=torch.float16))
+
+
+def test_python_wrappers_reject_mixed_devices():
+    torch = pytest.importorskip("torch")
+    from decodebench_amd import ops
+
+    a = torch.zeros(4)
+    ops._same_device((a, "x"), (torch.zeros(2), "W"))  # one device: accepted
+    with pytest.raises(ValueError, match="W is on meta"):
+        ops._same_device((a, "x"), (torch.zeros(2, device="meta"), "W"))
