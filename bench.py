@@ -19,7 +19,9 @@ the 256 MB Infinity Cache), so every step streams its weights from HBM.
                  calls replayed from a hipGraph
   decomposition  Sequence.profile of the unfused torch stages (stream and
                  graph) against the fused kernels: Delta_launch and B, for
-                 F1, F2, F4 and the decode layer (fp16 and fp8 weights)
+                 F1, F2, F4 and the decode layer (fp16 and fp8 weights),
+                 with the per-trial samples and a fused-vs-unfused output
+                 check that decodebench_amd.validate reads
   cpu_baseline   the torch CPU restatement of the reference stages
                  (oracle/stages.py) on this host's cores, F2 at full size
 
@@ -61,11 +63,14 @@ def parse_args(argv=None):
                          "decomposition and the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bound on the CPU baseline sample")
-    ap.add_argument("--trials", type=int, default=12,
-                    help="trials per variant in the decomposition")
+    ap.add_argument("--trials", type=int, default=30,
+                    help="trials per variant in the decomposition (the validation report "
+                         "needs >= 30)")
     ap.add_argument("--profile-pass", metavar="MANIFEST",
                     help="run the workload for rocprofv3 instead: calibration copies, then "
-                         "every kernel eagerly; write the launch manifest to MANIFEST and exit")
+                         "every fused workload and the decomposition configs' unfused stage "
+                         "chains eagerly, each between two delimiter kernels; write the launch "
+                         "manifest to MANIFEST and exit")
     ap.add_argument("--sweep-only", metavar="REGEX",
                     help="per-kernel table restricted to matching workloads; skips the "
                          "decomposition and the CPU baseline")
@@ -147,6 +152,23 @@ def check_case(case) -> float:
     return float((out - ref).norm() / ref.norm().clamp_min(1e-30))
 
 
+def fused_check(case) -> dict:
+    """The fused output against the unfused torch stages on the same inputs,
+    with Sequence.profile's elementwise bar (abs < 5e-2 or rel < 2e-2)."""
+    import torch
+
+    from decodebench_amd.sequence import _FUSED_ABS_TOL, _FUSED_REL_TOL
+
+    ref = case.seq._replay_body(case.replicas[0]).float()
+    out = case.fused(case.replicas[0]).float()
+    err = (out - ref).abs()
+    rel = err / ref.abs().clamp_min(1e-12)
+    ok = bool(((err < _FUSED_ABS_TOL) | (rel < _FUSED_REL_TOL)).all())
+    torch.cuda.synchronize()
+    return {"ok": ok, "max_abs": float(err.max()),
+            "rel_l2": float((out - ref).norm() / ref.norm().clamp_min(1e-30))}
+
+
 def kernel_row(case, us: float) -> dict:
     gbs = case.algorithmic_bytes / (us * 1e-6) / 1e9
     tflops = case.flops / (us * 1e-6) / 1e12
@@ -196,6 +218,14 @@ PROFILE_WORKLOADS = (("f1_cfg1", dict(name="f1")), ("f1_qkv_cfg3", dict(name="f1
                      ("f2_cfg2_B16", dict(name="f2", batch=16)),
                      ("f2_cfg2_fp8_B16", dict(name="f2", batch=16, dtype="fp8")))
 
+# The decomposition configs: Sequence.profile of the torch stages against
+# the fused call; their unfused stage chains are also profiled (τ_u and the
+# unfused bytes of decodebench_amd.validate).
+DECOMP_WORKLOADS = (("f1_cfg1", dict(name="f1")), ("f2_cfg2", dict(name="f2")),
+                    ("f4_L8192", dict(name="f4", L=8192)),
+                    ("layer_cfg5", dict(name="layer", L=8192)),
+                    ("layer_cfg5_fp8", dict(name="layer", L=8192, dtype="fp8")))
+
 
 def kernels_per_call(kw: dict) -> int:
     """Kernel launches of one fused call (F4 with S > 1 is two launches; the
@@ -213,13 +243,41 @@ def kernels_per_call(kw: dict) -> int:
     return 1
 
 
+def f4_partial_bytes(kw: dict, batch: int = 1) -> int:
+    """HBM bytes a fused F4 call adds over a single-pass kernel: the split
+    partial records (o, m, l per head and split) written by the first launch
+    and read back by the merge."""
+    from decodebench_amd import ops
+    from decodebench_amd.demos.llama_decode import LAYER
+
+    if kw["name"] not in ("f4", "layer"):
+        return 0
+    Hq, Hkv, D = LAYER["Hq"], LAYER["Hkv"], LAYER["D"]
+    S = ops.f4_default_splits(batch, Hkv, kw.get("L", 8192))
+    return 0 if S <= 1 else 2 * batch * Hq * S * (D + 2) * 4
+
+
 def profile_pass(manifest_path: str, calls: int = 24, warmup: int = 4) -> int:
     """Launch sequence for decodebench_amd.rocprof: calibration copies first,
-    then each workload's fused kernels eagerly over cache-defeating replicas."""
+    then each workload's calls eagerly over cache-defeating replicas, between
+    two launches of the library's empty kernel (the segment delimiters).  The
+    fused calls of every profile workload come first, then the unfused torch
+    stage chains of the decomposition configs.  Two warm-up calls precede
+    each segment, outside its delimiters."""
     import torch
 
     from decodebench_amd import ops
+    from decodebench_amd.bytes_model import eliminable_bytes, total_bytes
     from decodebench_amd.demos.llama_decode import build_config
+
+    def segment(body, n):
+        for i in range(2):
+            body(n - 1 - i)  # warm-up, on replicas the first calls do not use first
+        ops.null_kernel()
+        for i in range(calls):
+            body(i)
+        ops.null_kernel()
+        torch.cuda.synchronize()
 
     ops.load_library()
     copy_bytes, copy_calls = 512 << 20, 3
@@ -233,20 +291,30 @@ def profile_pass(manifest_path: str, calls: int = 24, warmup: int = 4) -> int:
     workloads = []
     for label, kw in PROFILE_WORKLOADS:
         case = build_config(gen_device="cuda", **{"batch": 1, **kw})
-        per_call = kernels_per_call(kw)
         n = len(case.replicas)
-        for i in range(calls):
-            case.fused(case.replicas[i % n])
-        torch.cuda.synchronize()
-        workloads.append({"label": label, "calls": calls, "warmup": warmup,
-                          "kernels_per_call": per_call,
+        segment(lambda i: case.fused(case.replicas[i % n]), n)
+        workloads.append({"label": label, "kind": "fused", "calls": calls, "warmup": warmup,
+                          "kernels_per_call": kernels_per_call(kw),
                           "algorithmic_bytes": case.algorithmic_bytes})
         log(f"profile pass: {label} x {calls}")
         del case
         torch.cuda.empty_cache()
+    for label, kw in DECOMP_WORKLOADS:
+        case = build_config(gen_device="cuda", **{"batch": 1, **kw})
+        traces = case.seq.trace(case.inputs)
+        n = len(case.replicas)
+        # the stage chain as Sequence.profile's stream variant runs it
+        segment(lambda i: case.seq._replay_body(case.replicas[i % n]), n)
+        workloads.append({"label": f"{label}_unfused", "kind": "unfused", "calls": calls,
+                          "warmup": warmup, "kernels_per_call": None,
+                          "algorithmic_bytes": total_bytes(traces),
+                          "eliminable_bytes": eliminable_bytes(traces)})
+        log(f"profile pass: {label}_unfused x {calls}")
+        del case
+        torch.cuda.empty_cache()
     with open(manifest_path, "w") as f:
         json.dump({"copy_bytes": copy_bytes, "copy_calls": copy_calls,
-                   "workloads": workloads}, f, indent=1)
+                   "delimiter": "null_kernel", "workloads": workloads}, f, indent=1)
     return 0
 
 
@@ -384,10 +452,7 @@ def main(argv=None) -> int:
     if not args.quick and not args.sweep_only:
         # ---- Delta_launch vs B: unfused stream / graph vs fused ----------
         decomp = {}
-        for name, kw in (("f1_cfg1", dict(name="f1")), ("f2_cfg2", dict(name="f2")),
-                         ("f4_L8192", dict(name="f4", L=8192)),
-                         ("layer_cfg5", dict(name="layer", L=8192)),
-                         ("layer_cfg5_fp8", dict(name="layer", L=8192, dtype="fp8"))):
+        for name, kw in DECOMP_WORKLOADS:
             case = build_config(batch=1, gen_device="cuda", **kw)
             rep = case.seq.profile(case.inputs, trials=args.trials, target_ms=10.0,
                                    warmup=10, input_replicas=case.replicas,
@@ -399,7 +464,11 @@ def main(argv=None) -> int:
                 "delta_launch_ci": [round(c, 3) for c in v.delta_launch_ci],
                 "B_us": round(v.b_bytes_est, 3), "residual_us": round(v.residual_us, 3),
                 "bound": v.bound, "dominant": v.dominant,
-                "total_bytes": v.total_bytes, "eliminable_bytes": v.eliminable_bytes}
+                "total_bytes": v.total_bytes, "eliminable_bytes": v.eliminable_bytes,
+                "fused_extra_bytes": f4_partial_bytes(kw),
+                "fused_check": fused_check(case),
+                "samples_us": {k: [round(t, 3) for t in getattr(rep, f"{k}_us")]
+                               for k in ("stream", "graph", "fused")}}
             log(f"{name}: stream {v.t_stream:.2f} graph {v.t_graph:.2f} fused "
                 f"{v.t_fused:.2f} us; dL {v.delta_launch:.2f} B {v.b_bytes_est:.3f}")
             del case, rep

@@ -11,6 +11,23 @@ which writes a manifest of what it launched, in order:
   2. for each workload, ``calls`` fused calls of ``kernels_per_call`` HIP
      kernels of this library each, over cache-defeating replicas.
 
+Workloads are of two kinds.  *Fused* workloads are calls of this library's
+kernels; *unfused* workloads are calls of the reference's torch stage chain
+(an unknown number of torch kernels per call) on the same inputs, whose
+per-round kernel time τ_u and HBM bytes feed the decomposition checks of
+``decodebench_amd.validate``.  The profiled program brackets every
+workload's calls between two launches of the library's empty kernel
+(``db_null_kernel``, the ``delimiter`` the manifest names), so a workload is
+the dispatches between its two delimiters, whatever launched them; warm-up
+calls made between workloads fall outside every segment.  Within a segment
+the calls are the rounds: the dispatch count must be a whole number of
+calls, and the kernel-name sequence must be periodic with a period that
+divides a call (:func:`find_round_size`, the reference's round detection,
+parse_ncu.py:26-48) -- a profiler-injected or stray kernel makes the
+profile fail instead of silently shifting rounds.  Manifests without a
+``delimiter`` (older profiles) match the library's dispatches in launch
+order instead.
+
 Three rocprofv3 runs of that program feed :func:`summarize`: ``--kernel-trace``
 (durations), ``--pmc FETCH_SIZE`` and ``--pmc WRITE_SIZE`` (KiB per dispatch,
 one counter per run).  Both counters are scaled by what they read for the
@@ -37,6 +54,7 @@ from pathlib import Path
 
 LIB_TAG = "dbk::"
 COPY_TAG = "copyBuffer"
+DELIM_TAG = "null_kernel"
 
 
 @dataclass
@@ -98,10 +116,60 @@ def read_counters(path) -> list[Dispatch]:
     return [by_id[k] for k in sorted(by_id)]
 
 
-def split_workloads(dispatches: list[Dispatch], manifest: dict) -> dict[str, list[list[Dispatch]]]:
-    """Assign the library's dispatches to the manifest's workloads, in order.
+def find_round_size(names: list[str]) -> int:
+    """Smallest period of a kernel-name sequence (the reference's round
+    detection, validation/analysis/parse_ncu.py:26-48): [a, b, a, b] -> 2,
+    [a, a, a] -> 1.  A sequence with no period raises ValueError."""
+    n = len(names)
+    for period in range(1, n // 2 + 1):
+        if all(names[i] == names[i % period] for i in range(n)):
+            return period
+    if n >= 1 and len(set(names)) == 1:
+        return 1
+    raise ValueError(
+        "kernel sequence is not periodic; cannot group rounds reliably. "
+        f"Distinct kernels: {sorted(set(names))[:8]}. First 12: {names[:12]}")
 
+
+def split_segments(dispatches: list[Dispatch],
+                   manifest: dict) -> dict[str, list[list[Dispatch]]]:
+    """Workloads as the dispatches between their begin and end delimiters.
+
+    Returns ``{label: [[dispatches of call 0], [call 1], ...]}``; raises
+    ValueError when the delimiters, the call count or the round structure do
+    not match the manifest."""
+    tag = manifest["delimiter"]
+    marks = [i for i, d in enumerate(dispatches) if tag in d.name]
+    work = manifest["workloads"]
+    if len(marks) != 2 * len(work):
+        raise ValueError(f"profile has {len(marks)} '{tag}' delimiters, manifest expects "
+                         f"{2 * len(work)} (two per workload)")
+    out = {}
+    for j, w in enumerate(work):
+        label, calls = w["label"], w["calls"]
+        seg = dispatches[marks[2 * j] + 1:marks[2 * j + 1]]
+        if not seg or len(seg) % calls:
+            raise ValueError(f"{label}: {len(seg)} dispatches are not {calls} whole calls")
+        per = len(seg) // calls
+        k = w.get("kernels_per_call")
+        if k is not None and per != k:
+            raise ValueError(f"{label}: {per} kernels per call, manifest expects {k}")
+        period = find_round_size([d.name for d in seg])
+        if per % period:
+            raise ValueError(f"{label}: kernel sequence period {period} does not divide the "
+                             f"{per} kernels of a call")
+        out[label] = [seg[i * per:(i + 1) * per] for i in range(calls)]
+    return out
+
+
+def split_workloads(dispatches: list[Dispatch], manifest: dict) -> dict[str, list[list[Dispatch]]]:
+    """Assign the dispatches to the manifest's workloads.
+
+    With a ``delimiter`` in the manifest, see :func:`split_segments`;
+    otherwise the library's dispatches are taken in launch order.
     Returns ``{label: [[dispatches of call 0], [call 1], ...]}``."""
+    if manifest.get("delimiter"):
+        return split_segments(dispatches, manifest)
     ours = [d for d in dispatches if LIB_TAG in d.name]
     need = sum(w["calls"] * w["kernels_per_call"] for w in manifest["workloads"])
     if len(ours) != need:
@@ -134,17 +202,24 @@ def summarize(manifest: dict, trace=None, fetch=None, write=None) -> dict:
     per: dict[str, dict] = {w["label"]: {"algorithmic_bytes": w["algorithmic_bytes"]}
                             for w in manifest["workloads"]}
     warm = {w["label"]: w.get("warmup", 0) for w in manifest["workloads"]}
+    kind = {w["label"]: w.get("kind", "fused") for w in manifest["workloads"]}
+    for w in manifest["workloads"]:
+        per[w["label"]]["kind"] = kind[w["label"]]
     if trace is not None:
         tw = split_workloads(trace, manifest)
         for label, calls in tw.items():
             calls = calls[warm[label]:]
-            kern = {}
-            for j, d in enumerate(calls[0]):
-                durs = [c[j].duration_ns for c in calls]
-                kern[short_name(d.name)] = statistics.median(durs) / 1e3
+            if not calls:
+                raise ValueError(f"{label}: no calls left after {warm[label]} warm-up calls")
             total = statistics.median(sum(d.duration_ns for d in c) for c in calls) / 1e3
-            per[label].update({"kernel_us": kern, "call_us": total,
+            per[label].update({"call_us": total, "kernels_per_call": len(calls[0]),
                                "GB/s": per[label]["algorithmic_bytes"] / (total * 1e3)})
+            if kind[label] == "fused":
+                kern = {}
+                for j, d in enumerate(calls[0]):
+                    durs = [c[j].duration_ns for c in calls]
+                    kern[short_name(d.name)] = statistics.median(durs) / 1e3
+                per[label]["kernel_us"] = kern
     for counter, disp, key in (("FETCH_SIZE", fetch, "fetch_bytes"),
                                ("WRITE_SIZE", write, "write_bytes")):
         if disp is None:
@@ -154,6 +229,8 @@ def summarize(manifest: dict, trace=None, fetch=None, write=None) -> dict:
         cw = split_workloads(disp, manifest)
         for label, calls in cw.items():
             calls = calls[warm[label]:]
+            if not calls:
+                raise ValueError(f"{label}: no calls left after {warm[label]} warm-up calls")
             per[label][key] = statistics.median(
                 sum(d.counters[counter] for d in c) * 1024.0 * scale for c in calls)
     for label, p in per.items():
@@ -173,11 +250,20 @@ def to_markdown(res: dict, command: str) -> str:
                      f"{res.get('WRITE_SIZE_scale', float('nan')):.3f} bytes per KiB-unit "
                      "(factors applied below).")
         lines.append("")
+    if any(p.get("kind") == "unfused" for p in res["workloads"].values()):
+        lines.append("Rows ending in `_unfused` are the torch stage chain of the same config "
+                     "(kernel time summed over a call); their 'Algorithmic B' is the byte "
+                     "model's total (`bytes_model.total_bytes` of the stage traces).")
+        lines.append("")
     lines += ["| Workload | Kernel us (median) | Call us | Algorithmic B | GB/s | % of 8 TB/s | "
               "Fetch B | Write B | Traffic / algorithmic |",
               "|---|---|---|---|---|---|---|---|---|"]
     for label, p in res["workloads"].items():
-        ku = "; ".join(f"{k.split('::')[-1]} {v:.2f}" for k, v in p.get("kernel_us", {}).items())
+        if p.get("kind") == "unfused":
+            ku = f"{p.get('kernels_per_call', '?')} torch kernels (unfused stages)"
+        else:
+            ku = "; ".join(f"{k.split('::')[-1]} {v:.2f}"
+                           for k, v in p.get("kernel_us", {}).items())
         call = p.get("call_us")
         gbs = p.get("GB/s")
         lines.append(

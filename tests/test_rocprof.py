@@ -100,3 +100,90 @@ def test_mismatched_profile_fails(files):
     with pytest.raises(ValueError, match="calibration"):
         rocprof.summarize(dict(MANIFEST, copy_calls=5),
                           fetch=rocprof.read_counters(files / "f.csv"))
+
+
+# ------------------------------------------------ delimited segments
+# The profile pass brackets every workload between two launches of the
+# library's empty kernel; warm-up calls sit outside the brackets, and an
+# unfused workload is whatever torch launched inside them.
+NULL = "(anonymous namespace)::null_kernel()"
+SEG_MANIFEST = {
+    "copy_bytes": 1 << 20, "copy_calls": 1, "delimiter": "null_kernel",
+    "workloads": [
+        {"label": "f1", "kind": "fused", "calls": 2, "warmup": 0, "kernels_per_call": 1,
+         "algorithmic_bytes": 1000},
+        {"label": "f1_unfused", "kind": "unfused", "calls": 2, "warmup": 0,
+         "kernels_per_call": None, "algorithmic_bytes": 3000},
+    ],
+}
+SEG_ROWS = [
+    ("__amd_rocclr_copyBuffer", 900, 512.0, 1024.0),
+    ("void dbk::(anonymous namespace)::gemv_kernel<1>(args)", 7000, 9.0, 9.0),  # warm-up
+    (NULL, 5, 0.0, 0.0),
+    ("void dbk::(anonymous namespace)::gemv_kernel<1>(args)", 2000, 0.5, 0.25),
+    ("void dbk::(anonymous namespace)::gemv_kernel<1>(args)", 4000, 0.5, 0.25),
+    (NULL, 5, 0.0, 0.0),
+    ("void at::native::reduce_kernel", 9000, 5.0, 5.0),                          # warm-up
+    (NULL, 5, 0.0, 0.0),
+    ("void at::native::reduce_kernel", 1000, 1.0, 0.0),
+    ("void at::native::elementwise_kernel", 500, 0.5, 0.5),
+    ("Cijk_gemv", 3000, 1.0, 0.5),
+    ("void at::native::reduce_kernel", 1000, 1.0, 0.0),
+    ("void at::native::elementwise_kernel", 700, 0.5, 0.5),
+    ("Cijk_gemv", 3000, 1.0, 0.5),
+    (NULL, 5, 0.0, 0.0),
+]
+
+
+def _write_rows(tmp_path, rows):
+    global ROWS
+    saved, ROWS = ROWS, rows
+    try:
+        write_trace(tmp_path / "t.csv")
+        write_counters(tmp_path / "f.csv", "FETCH_SIZE", 2)
+        write_counters(tmp_path / "w.csv", "WRITE_SIZE", 3)
+    finally:
+        ROWS = saved
+    return (rocprof.read_trace(tmp_path / "t.csv"), rocprof.read_counters(tmp_path / "f.csv"),
+            rocprof.read_counters(tmp_path / "w.csv"))
+
+
+def test_round_detection_matches_the_reference_examples():
+    assert rocprof.find_round_size(["rmsnorm", "gemv", "rmsnorm", "gemv"]) == 2
+    assert rocprof.find_round_size(["gemv", "gemv", "swiglu"] * 2) == 3
+    assert rocprof.find_round_size(["f1"] * 5) == 1
+    assert rocprof.find_round_size(["f1"]) == 1
+    with pytest.raises(ValueError, match="not periodic"):
+        rocprof.find_round_size(["a", "b", "a", "c"])
+
+
+def test_delimited_segments_hold_fused_and_unfused_calls(tmp_path):
+    trace, fetch, write = _write_rows(tmp_path, SEG_ROWS)
+    res = rocprof.summarize(SEG_MANIFEST, trace=trace, fetch=fetch, write=write)
+    f1, un = res["workloads"]["f1"], res["workloads"]["f1_unfused"]
+    assert f1["call_us"] == pytest.approx(3.0) and f1["kind"] == "fused"
+    # three torch kernels per call, warm-up outside the brackets ignored
+    assert un["kernels_per_call"] == 3 and un["kind"] == "unfused"
+    assert un["call_us"] == pytest.approx((4.5 + 4.7) / 2)
+    assert un["fetch_bytes"] == pytest.approx(2.5 * 1024 * 2)
+    assert un["write_bytes"] == pytest.approx(1.0 * 1024)
+    assert "kernel_us" not in un
+    assert "3 torch kernels" in rocprof.to_markdown(res, "cmd")
+
+
+def test_segments_fail_closed(tmp_path):
+    # a missing end delimiter
+    trace, _, _ = _write_rows(tmp_path, SEG_ROWS[:-1])
+    with pytest.raises(ValueError, match="delimiters"):
+        rocprof.summarize(SEG_MANIFEST, trace=trace)
+    # a stray kernel inside the unfused segment breaks its rounds
+    rows = SEG_ROWS[:-1] + [("void at::native::fill", 10, 0.0, 0.0), (NULL, 5, 0.0, 0.0)]
+    trace, _, _ = _write_rows(tmp_path, rows)
+    with pytest.raises(ValueError, match="whole calls|not periodic|period"):
+        rocprof.summarize(SEG_MANIFEST, trace=trace)
+    # a fused call with an unexpected kernel count
+    bad = {**SEG_MANIFEST, "workloads": [dict(SEG_MANIFEST["workloads"][0], kernels_per_call=2),
+                                         SEG_MANIFEST["workloads"][1]]}
+    trace, _, _ = _write_rows(tmp_path, SEG_ROWS)
+    with pytest.raises(ValueError, match="kernels per call"):
+        rocprof.summarize(bad, trace=trace)
