@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
 
-Prints ONE JSON line.  The headline workload is BASELINE config 2 at batch 1:
+Prints ONE JSON line.  The headline workload is the benchmark's config 2 at batch 1:
 F2 = gate/up GEMV + SwiGLU, x[1,4096] fp16, Wg/Wu[14336,4096] fp16 ~N(0,0.02).
 A step is one fused launch over a fresh weight replica; the replicas rotate
 through a working set larger than twice the on-die caches (8 x 4 MB L2 plus
@@ -180,7 +180,7 @@ def kernel_row(case, us: float) -> dict:
 
 
 def sweep_workloads():
-    """BASELINE configs 1-4 with their batch, KV-length and split sweeps."""
+    """Benchmark configs 1-4 with their batch, KV-length and split sweeps."""
     out = [("f1_cfg1", dict(name="f1", batch=1))]
     for B in (1, 4, 8, 16, 32):
         out.append((f"f1_qkv_cfg3" + ("" if B == 1 else f"_B{B}"), dict(name="f1_qkv", batch=B)))
@@ -416,7 +416,7 @@ def main(argv=None) -> int:
         "scaling": "weak", "vs_baseline": None, "dtype": "f16",
         "data": "synthetic (seeded torch.Generator(42), fp32 -> fp16)",
         "config": {"workload": "F2 gate/up GEMV + SwiGLU fused, batch 1, x[1,4096], "
-                               "Wg/Wu[14336,4096] fp16 (BASELINE configs[1])",
+                               "Wg/Wu[14336,4096] fp16 (benchmark configs[1])",
                    "batch": 1, "K": 4096, "N": 14336,
                    "weight_replicas": len(head.replicas), "device": dev_name},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,

@@ -23,7 +23,7 @@ The printed lines follow calibrate.cu's output ("t_launch_stream: ... us",
 
 One comparison has no counterpart in the reference: :func:`vendor_f4` times
 F4 (``db_f4_splitkv``) against torch's ``scaled_dot_product_attention`` at
-the BASELINE decode shape (32 query heads, 8 KV heads, head dim 128, fp16,
+the benchmark's decode shape (32 query heads, 8 KV heads, head dim 128, fp16,
 Q/K/V ~ N(0, 1)), both replayed back to back in a hipGraph over
 cache-defeating KV replicas, and reports their largest output difference as
 an independent cross-check of F4's results.

@@ -400,7 +400,7 @@ def _weight(gen, shape, std, device, fp8: bool):
 def build_config(name: str, batch: int = 1, L: int = 8192, n_splits: int | None = None,
                  seed: int = 42, device="cuda", replicas: int | None = None,
                  K: int = 4096, gen_device: str = "cpu", dtype: str = "f16") -> Case:
-    """BASELINE-shaped case; ``replicas=None`` sizes a cache-defeating rotation.
+    """A case at the benchmark's shapes (configs 1-5); ``replicas=None`` sizes a cache-defeating rotation.
 
     ``gen_device="cpu"`` draws the inputs on the CPU (device-independent
     values, what the parity tests use); ``"cuda"`` draws them on the GPU.

@@ -9,7 +9,7 @@ loudly when its HIP library is missing instead of falling back to the CPU.
 Contents
   stages.py  the reference's PyTorch stage definitions restated for CPU
              tensors (src/decodebench/demos/llama_decode.py:36-43, 77-87,
-             120-134) with the BASELINE settings: eps 1e-6, scale 1/sqrt(D),
+             120-134) with the benchmark's settings: eps 1e-6, scale 1/sqrt(D),
              grouped-query attention; plus the decode-layer chain.
   cref.c     plain-C restatement with double accumulation and explicit fp16
              rounding points; cref.py is its ctypes/numpy wrapper.

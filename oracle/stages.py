@@ -5,7 +5,7 @@ the north-star parity criterion names: the fused HIP kernels must match them
 on the same seeded inputs within rtol 1e-2 / atol 1e-2.
 
 Each stage restates a stage body of src/decodebench/demos/llama_decode.py
-with the BASELINE settings the reference leaves open:
+with the benchmark's settings where the reference leaves them open:
   * rmsnorm eps 1e-6 (llama_decode.py:39 already uses 1e-6);
   * attention scale 1/sqrt(D) applied to the fp32 scores (the reference demo
     has no scale, llama_decode.py:125; its CUDA kernels and harness oracle do,

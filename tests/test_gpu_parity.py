@@ -1,6 +1,6 @@
 """Parity of the HIP kernels (through the C ABI) with the CPU oracle.
 
-Bar: outputs within rtol 1e-2 / atol 1e-2 of the
+Bar (the benchmark's parity target): outputs within rtol 1e-2 / atol 1e-2 of the
 reference's PyTorch stage definitions (oracle/stages.py, run on CPU with the
 same seeded fp16 inputs).  Because atol 1e-2 is weak where outputs are small
 (F4 at long context), every case also checks the relative L2 error against
