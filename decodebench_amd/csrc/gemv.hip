@@ -107,8 +107,9 @@ hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
     if (e != hipSuccess) return e;
   }
   const int waves = pick_waves(a.groups, cu_count);
-  dim3 grid((waves + kGemvWaves - 1) / kGemvWaves, (B + nb - 1) / nb);
-  hipLaunchKernelGGL(fn, grid, dim3(kGemvThreads), lds, stream, a);
+  const int wv = gemv_wg_waves(mode, w.fp8, nb);
+  dim3 grid((waves + wv - 1) / wv, (B + nb - 1) / nb);
+  hipLaunchKernelGGL(fn, grid, dim3(wv * kWave), lds, stream, a);
   return hipGetLastError();
 }
 

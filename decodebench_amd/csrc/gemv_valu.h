@@ -2,7 +2,8 @@
 // gfx950, shared by the fp16-weight (gemv.hip) and fp8-weight (gemv_fp8.hip)
 // translation units, which instantiate disjoint halves of it.
 //
-//  * A workgroup is 4 waves.  The activation rows it needs (x, or the
+//  * A workgroup is 4 waves (1 for the fp16 gate/up pair at one batch row,
+//    see gemv_wg_waves).  The activation rows it needs (x, or the
 //    RMS-normalised x) are built ONCE per workgroup in LDS; the normalised
 //    vector never goes to HBM.
 //  * Each wave owns groups of R consecutive weight rows and streams them with
@@ -36,8 +37,15 @@
 
 namespace dbk {
 
-constexpr int kGemvThreads = 256;
-constexpr int kGemvWaves = kGemvThreads / kWave;
+// Waves per workgroup.  Measured on MI355X at K = 4096, one batch row
+// (graph back-to-back, interleaved runs): the fp16 gate/up pair streams
+// fastest with single-wave workgroups, which start and retire independently
+// (F2 35.2 -> 33.9 us, RMSNorm->F2 36.3 -> 35.7 us); every other mode, batch
+// and weight type is fastest with 4 waves sharing one activation prologue
+// (single waves cost up to 1.5x on the e4m3 projections and F1).
+constexpr int gemv_wg_waves(int mode, bool fp8, int nb) {
+  return (!fp8 && gemv_is_swiglu(mode) && nb == 1) ? 1 : 4;
+}
 
 struct GemvArgs {
   const _Float16* x;      // [B, K]
@@ -94,12 +102,12 @@ __device__ __forceinline__ void e4m3x16_to_h(const u4& w, u4& lo, u4& hi) {
   hi[3] = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[3], 1.0f, true));
 }
 
-template <int MODE, int NB, int R, int U, bool FP8>
-__global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
+template <int MODE, int NB, int R, int U, bool FP8, int WV>
+__global__ __launch_bounds__(WV * kWave) void gemv_kernel(GemvArgs a) {
   constexpr bool kNorm = gemv_has_norm(MODE);
   constexpr int NW = gemv_is_swiglu(MODE) ? 2 : 1;  // weight matrices
-  constexpr int kThreads = kGemvThreads;
-  constexpr int kWaves = kGemvWaves;
+  constexpr int kThreads = WV * kWave;
+  constexpr int kWaves = WV;
   extern __shared__ __align__(16) unsigned char lds_raw[];
   u4* xs = reinterpret_cast<u4*>(lds_raw);           // [NB][kp8]
   __shared__ float red[kWaves][NB];
@@ -151,7 +159,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
   // behind it (loads complete in issue order).  The loads are unconditional
   // (clamped addresses, masked afterwards) and their uses straight-line, so
   // the compiler waits for them alone and not for the weights.
-  constexpr int kPre = 2;  // covers K <= 2 * 256 * 8 = 4096 with no reload
+  // Passes of 16-byte chunks per thread covering K <= 4096 with no reload.
+  constexpr int kPre = 512 / kThreads >= 1 ? 512 / kThreads : 1;
   static_assert((kPre * kThreads & (kPre * kThreads - 1)) == 0, "slot count: power of 2");
   // Pass i of thread t fills chunk pre_chunk(i), a permutation of the
   // kPre * kThreads slots rotated by 1 KB per workgroup: workgroups on one
@@ -230,7 +239,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
     float inv[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      const float tot = (red[0][b] + red[1][b]) + (red[2][b] + red[3][b]);
+      float tot = 0.0f;
+#pragma unroll
+      for (int v = 0; v < kWaves; ++v) tot += red[v][b];
       inv[b] = 1.0f / sqrtf(tot / (float)a.K + a.eps);
     }
     // fp16(x * inv_rms), then fp16(that * gamma): the fp16 x fp16 product is
@@ -384,12 +395,13 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
 // lane, with R fixed by gemv_rows_per_group.
 template <int MODE, int NB, bool FP8>
 GemvFn gemv_pick_u(int u) {
+  constexpr int WV = gemv_wg_waves(MODE, FP8, NB);
   switch (u) {
-    case 1: return gemv_kernel<MODE, NB, gemv_rows_per_group(MODE, FP8, 1), 1, FP8>;
-    case 2: return gemv_kernel<MODE, NB, gemv_rows_per_group(MODE, FP8, 2), 2, FP8>;
-    case 4: return gemv_kernel<MODE, NB, gemv_rows_per_group(MODE, FP8, 4), 4, FP8>;
-    case 7: return gemv_kernel<MODE, NB, gemv_rows_per_group(MODE, FP8, 7), 7, FP8>;
-    default: return gemv_kernel<MODE, NB, gemv_rows_per_group(MODE, FP8, 8), 8, FP8>;
+    case 1: return gemv_kernel<MODE, NB, gemv_rows_per_group(MODE, FP8, 1), 1, FP8, WV>;
+    case 2: return gemv_kernel<MODE, NB, gemv_rows_per_group(MODE, FP8, 2), 2, FP8, WV>;
+    case 4: return gemv_kernel<MODE, NB, gemv_rows_per_group(MODE, FP8, 4), 4, FP8, WV>;
+    case 7: return gemv_kernel<MODE, NB, gemv_rows_per_group(MODE, FP8, 7), 7, FP8, WV>;
+    default: return gemv_kernel<MODE, NB, gemv_rows_per_group(MODE, FP8, 8), 8, FP8, WV>;
   }
 }
 
