@@ -296,19 +296,23 @@ def f4_default_splits(B: int, Hkv: int, L: int, device=None) -> int:
 
 
 def f4_workspace(B: int, Hq: int, Hkv: int, L: int, D: int, S: int, device):
-    """Workspace for db_f4_splitkv, cached per size and device.
+    """Workspace for db_f4_splitkv, cached per size, device and current stream.
 
     It is zero-filled once, when allocated; every call leaves its split
     tickets at zero again, so one buffer serves every later call of that size
-    on that device, also under graph capture (calls sharing it must not
-    overlap in time)."""
+    on that stream, whose calls run in order, also under graph capture.
+    Calls on different streams get different buffers, so they may overlap.
+    (Replays of two graphs captured on one stream share its buffer and must
+    not overlap.)  torch draws streams from a fixed pool per device, so the
+    cache stays bounded."""
     import torch
 
     nbytes = int(load_library().db_f4_workspace_bytes(B, Hq, Hkv, L, D, S))
     if nbytes == 0:
         return None
     dev = torch.device(device)
-    key = (dev.index if dev.index is not None else torch.cuda.current_device(), nbytes)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (idx, torch.cuda.current_stream(idx).cuda_stream, nbytes)
     ws = _ws_cache.get(key)
     if ws is None:
         ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)

@@ -418,6 +418,33 @@ def test_f4_workspace_reuse_is_deterministic():
     assert int(ws[:256].count_nonzero()) == 0
 
 
+def test_f4_concurrent_streams_get_their_own_workspace():
+    """Two streams running F4 of one shape at the same time: the cached
+    workspace is per stream, so neither stream's split partials are
+    overwritten by the other's, and both match their single-stream result."""
+    inputs = [f4_inputs(1, 32, 8, 8192, 11 + i) for i in range(2)]
+    dev = [tuple(t.cuda() for t in inp) for inp in inputs]
+    ref = [ops.f4_flashdecode(*d) for d in dev]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    outs = [[], []]
+    for _ in range(10):
+        for i, s in enumerate(streams):
+            with torch.cuda.stream(s):
+                outs[i].append(ops.f4_flashdecode(*dev[i]))
+    torch.cuda.synchronize()
+    ws = [ops.f4_workspace(1, 32, 8, 8192, 128, ops.f4_default_splits(1, 8, 8192), "cuda")]
+    with torch.cuda.stream(streams[0]):
+        ws.append(ops.f4_workspace(1, 32, 8, 8192, 128, ops.f4_default_splits(1, 8, 8192),
+                                   "cuda"))
+    assert ws[0].data_ptr() != ws[1].data_ptr()
+    for i in range(2):
+        for o in outs[i]:
+            assert torch.equal(o, ref[i])
+
+
 @pytest.mark.parametrize("B,L", [(1, 1024), (1, 8192), (4, 8192), (8, 300)])
 def test_f4_in_launch_merge_matches_two_launch_merge(B, L):
     """The split merge done by the last split's workgroup (f4_merge = 1) and
