@@ -33,8 +33,9 @@
 //  * Norm modes: each wave sums x^2 over its slice, the 8 partial sums meet in LDS,
 //    and every wave normalises its own x registers exactly as the torch stage
 //    rounds: fp16(fp16(x * inv_rms) * gamma), gamma read from an LDS copy.
-// Batches above 16 run as passes of 16 (grid.y); each pass re-reads the
-// weights.
+// Batches above 16 run as passes (grid.y), each reading the weights: one
+// weight matrix takes 32-row passes when the LDS holds rows 16..31 of x next
+// to the partial sums (XB), otherwise passes are 16 rows.
 #include "gemv_valu.h"
 
 namespace dbk {
@@ -72,18 +73,33 @@ struct MfmaArgs {
 // of two k-steps after v_cvt_scalef32_pk_f16_fp8 widening.  The activations
 // are loaded in the same column order, so the dot products are unchanged;
 // the row scales multiply the reduced sums in the epilogue.
-template <int MODE, int KH, int BT, int UPS, bool SINGLE, bool FP8>
+// XB (one weight matrix, BT = 2): a pass is 32 batch rows.  Rows 16..31 get
+// two more column tiles whose activation slices are written once to LDS
+// (each wave its own, 16 KB x KH / 8 per wave) and read back per group, so
+// every weight tile feeds 32 rows instead of being re-read by a second
+// 16-row pass.
+template <int MODE, int KH, int BT, int UPS, bool SINGLE, bool FP8, bool XB>
 __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   constexpr int NWM = gemv_is_swiglu(MODE) ? 2 : 1;
   constexpr int KW = FP8 ? KH / 2 : KH;  // 16-byte weight loads per row and slice
-  // Dynamic LDS, [group < gpw][matrix][wave][batch < 8 BT][row]: the 8
-  // K-slice partial sums of every output of the workgroup.
-  extern __shared__ __align__(16) float part[];
+  static_assert(!XB || (BT == 2 && NWM == 1), "LDS batch tiles: one matrix, two register tiles");
+  constexpr int NBT = XB ? BT + 2 : BT;   // batch column tiles of 8 in a pass
+  constexpr int kPass = 8 * NBT;          // batch rows per pass
+  constexpr int kXbU4 = XB ? kWavesM * 2 * KH * kWave : 0;
+  // Dynamic LDS: [XB activation tiles: wave][tile][k-step][lane] u4, then
+  // the partial sums [group < gpw][matrix][wave][batch < kPass][row], the
+  // 8 K-slice partial sums of every output of the workgroup.
+  extern __shared__ __align__(16) unsigned char dyn_lds[];
+  u4* xbuf = reinterpret_cast<u4*>(dyn_lds);
+  float* part = reinterpret_cast<float*>(dyn_lds + (size_t)kXbU4 * 16);
   auto slot = [&](int j, int m, int v, int n) -> float* {
-    return part + ((((j * NWM + m) * kWavesM + v) * (8 * BT) + n) * kRowsPerGroup);
+    return part + ((((j * NWM + m) * kWavesM + v) * kPass + n) * kRowsPerGroup);
   };
-  __shared__ float red[kWavesM][kBatchTile];
-  __shared__ u4 s_gamma[gemv_has_norm(MODE) ? kThreadsM : 1];  // K / 8 chunks
+  __shared__ float red[kWavesM][kPass];
+  // gamma's LDS copy (K / 8 chunks): static, or with XB the start of the
+  // partial-sum region, which nothing writes before the prologue ends.
+  __shared__ u4 s_gamma_own[gemv_has_norm(MODE) && !XB ? kThreadsM : 1];
+  u4* const s_gamma = XB ? reinterpret_cast<u4*>(part) : s_gamma_own;
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -91,8 +107,8 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   const int g4 = lane >> 4;   // k-group
   const int r8 = c16 & 7;     // weight row in the group / batch row in the tile
   const int half = c16 >> 3;  // which half of the slice this lane covers
-  const int b0 = blockIdx.y * kBatchTile;
-  const int nb = min(kBatchTile, a.B - b0);
+  const int b0 = blockIdx.y * kPass;
+  const int nb = min(kPass, a.B - b0);
   // Wave v of workgroup w owns slice s = (v + w + w / 8) mod 8, columns
   // [s, s+1) * K / 8: workgroups on one XCD (w, w + 8, ...) and on
   // neighbouring XCDs start on different slices, so the 256 reads of x are
@@ -123,6 +139,17 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
 #pragma unroll
     for (int t = 0; t < KH; ++t)
       xr[bt][t] = ld16(a.x + (size_t)xrow * a.K + (FP8 ? xcol(t) : kcol + 64 * t));
+  }
+  // XB: rows 16..31 of the pass, in registers until they are written to LDS.
+  u4 xb[XB ? 2 : 1][KH];
+  if constexpr (XB) {
+#pragma unroll
+    for (int bt = 0; bt < 2; ++bt) {
+      const int xrow = b0 + min(16 + 8 * bt + r8, nb - 1);
+#pragma unroll
+      for (int t = 0; t < KH; ++t)
+        xb[bt][t] = ld16(a.x + (size_t)xrow * a.K + (FP8 ? xcol(t) : kcol + 64 * t));
+    }
   }
   u4 gchunk = {0, 0, 0, 0};
   if constexpr (gemv_has_norm(MODE))
@@ -167,11 +194,47 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
 #pragma unroll
     for (int t = 0; t < KH; ++t) xr[bt][t] = valid ? xr[bt][t] : zero4;
   }
+  if constexpr (XB) {
+#pragma unroll
+    for (int bt = 0; bt < 2; ++bt) {
+      const bool valid = 16 + 8 * bt + r8 < nb;
+#pragma unroll
+      for (int t = 0; t < KH; ++t) xb[bt][t] = valid ? xb[bt][t] : zero4;
+    }
+  }
   if constexpr (BT == 1) {
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x and gamma are here
   }
   __builtin_amdgcn_sched_barrier(0);
+
+  if constexpr (XB) {
+    // Rows 16..31: their x^2 sums (norm modes), then raw into their LDS
+    // tiles before set A is requested, so both halves of the pass and set A
+    // are never live together.  Each wave writes and later reads back only
+    // its own slots (LDS keeps a wave's accesses in order).
+#pragma unroll
+    for (int bt = 0; bt < 2; ++bt) {
+      if constexpr (gemv_has_norm(MODE)) {
+        float sb = 0.0f;
+#pragma unroll
+        for (int t = 0; t < KH; ++t)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const h2 p = as_h2(xb[bt][t][j]);
+            const float lo = (float)p[0], hi = (float)p[1];
+            sb += lo * lo + hi * hi;
+          }
+        sb += __shfl_xor(sb, 8);
+        sb += __shfl_xor(sb, 16);
+        sb += __shfl_xor(sb, 32);
+        if (lane < 8) red[wave][8 * (BT + bt) + lane] = sb;
+      }
+#pragma unroll
+      for (int t = 0; t < KH; ++t) xbuf[((wave * 2 + bt) * KH + t) * kWave + lane] = xb[bt][t];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   u4 wa[UPS][NWM][KW];
   load_set(wa, 0, true);  // every workgroup owns at least one group
@@ -199,6 +262,31 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
     }
     if ((int)threadIdx.x < a.K / 8) s_gamma[threadIdx.x] = gchunk;
     __syncthreads();
+    if constexpr (XB) {
+      // rows 16..31: normalised in place in their LDS tiles
+#pragma unroll
+      for (int bt = 0; bt < 2; ++bt) {
+        float tot = 0.0f;
+#pragma unroll
+        for (int v = 0; v < kWavesM; ++v) tot += red[v][8 * (BT + bt) + r8];
+        const float inv = 1.0f / sqrtf(tot / (float)a.K + a.eps);
+#pragma unroll
+        for (int t = 0; t < KH; ++t) {
+          const u4 gv = s_gamma[(FP8 ? xcol(t) : kcol + 64 * t) / 8];
+          const u4 xv = xbuf[((wave * 2 + bt) * KH + t) * kWave + lane];
+          u4 out;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const h2 xp = as_h2(xv[j]);
+            const h2 gp = as_h2(gv[j]);
+            const float n0 = (float)to_h((float)xp[0] * inv);
+            const float n1 = (float)to_h((float)xp[1] * inv);
+            out[j] = pack_h2(n0 * (float)gp[0], n1 * (float)gp[1]);
+          }
+          xbuf[((wave * 2 + bt) * KH + t) * kWave + lane] = out;
+        }
+      }
+    }
 #pragma unroll
     for (int bt = 0; bt < BT; ++bt) {
       float tot = 0.0f;
@@ -220,6 +308,9 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
         xr[bt][t] = out;
       }
     }
+    // gamma shares the partial-sum region under XB: every wave must be done
+    // with it before the first partial sum is stored.
+    if constexpr (XB) __syncthreads();
   }
 
   // ---- stream the groups ------------------------------------------------
@@ -254,6 +345,25 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
           if (g4 < 2 && c16 < 8)
             *reinterpret_cast<f4*>(slot(j, m, wave, 8 * bt + c16) + 4 * g4) = acc;
         }
+        if constexpr (XB) {
+          // rows 16..31: the same A operands against the LDS tiles
+#pragma unroll
+          for (int bt = 0; bt < 2; ++bt) {
+            f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int t = 0; t < KH; ++t) {
+              const u4 at = FP8 ? av[FP8 ? t : 0] : src[q][m][FP8 ? 0 : t];
+              const u4 bx = xbuf[((wave * 2 + bt) * KH + t) * kWave + lane];
+              acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, at),
+                                                           __builtin_bit_cast(h8, bx), acc, 0, 0,
+                                                           0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] += __shfl(acc[i], lane + 40);
+            if (g4 < 2 && c16 < 8)
+              *reinterpret_cast<f4*>(slot(j, m, wave, 8 * (BT + bt) + c16) + 4 * g4) = acc;
+          }
+        }
       }
     }
   };
@@ -283,10 +393,10 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   __syncthreads();
 
   // ---- reduce the 8 K-slices, epilogue, fp16 store ----------------------
-  const int nout = my_groups * 8 * BT * kRowsPerGroup;
+  const int nout = my_groups * kPass * kRowsPerGroup;
   for (int idx = threadIdx.x; idx < nout; idx += kThreadsM) {
-    const int jj = idx / (8 * BT * kRowsPerGroup);
-    const int n = (idx / kRowsPerGroup) % (8 * BT);
+    const int jj = idx / (kPass * kRowsPerGroup);
+    const int n = (idx / kRowsPerGroup) % kPass;
     const int r = idx % kRowsPerGroup;
     const int row = (blockIdx.x + gridDim.x * jj) * kRowsPerGroup + r;
     if (n >= nb || row >= a.N) continue;
@@ -322,21 +432,21 @@ MfmaFn pick_ups(int ups) {
     // The normalisation next to two batch tiles and a gate/up pair: one
     // group pair per alternating set.
     (void)ups;
-    return gemv_mfma_kernel<MODE, KH, BT, 1, false, FP8>;
+    return gemv_mfma_kernel<MODE, KH, BT, 1, false, FP8, false>;
   } else if constexpr (gemv_is_swiglu(MODE)) {
-    return ups == 2 ? gemv_mfma_kernel<MODE, KH, BT, 2, true, FP8>
-                    : gemv_mfma_kernel<MODE, KH, BT, 1, false, FP8>;
+    return ups == 2 ? gemv_mfma_kernel<MODE, KH, BT, 2, true, FP8, false>
+                    : gemv_mfma_kernel<MODE, KH, BT, 1, false, FP8, false>;
   } else if constexpr (MODE == kGemvRmsNorm && BT == 2) {
     // Two batch tiles of F1 leave no registers for a whole-workgroup set
     // next to the normalisation; always alternate two sets of 2 groups.
     (void)ups;
-    return gemv_mfma_kernel<MODE, KH, BT, 2, false, FP8>;
+    return gemv_mfma_kernel<MODE, KH, BT, 2, false, FP8, false>;
   } else {
     switch (ups) {
-      case 2: return gemv_mfma_kernel<MODE, KH, BT, 2, true, FP8>;
-      case 3: return gemv_mfma_kernel<MODE, KH, BT, 3, true, FP8>;
-      case 4: return gemv_mfma_kernel<MODE, KH, BT, 4, true, FP8>;
-      default: return gemv_mfma_kernel<MODE, KH, BT, 2, false, FP8>;
+      case 2: return gemv_mfma_kernel<MODE, KH, BT, 2, true, FP8, false>;
+      case 3: return gemv_mfma_kernel<MODE, KH, BT, 3, true, FP8, false>;
+      case 4: return gemv_mfma_kernel<MODE, KH, BT, 4, true, FP8, false>;
+      default: return gemv_mfma_kernel<MODE, KH, BT, 2, false, FP8, false>;
     }
   }
 }
@@ -351,8 +461,18 @@ MfmaFn pick_kh(int kh, int bt, int ups) {
   return kh == 4 ? pick_bt<MODE, 4, FP8>(bt, ups) : pick_bt<MODE, 8, FP8>(bt, ups);
 }
 
+// 32-row passes of one weight matrix (XB): one group per alternating set,
+// since both halves of the pass and set A are live at the normalisation.
+template <int MODE, bool FP8>
+MfmaFn pick_xb(int kh) {
+  return kh == 4 ? gemv_mfma_kernel<MODE, 4, 2, 1, false, FP8, true>
+                 : gemv_mfma_kernel<MODE, 8, 2, 1, false, FP8, true>;
+}
+
 template <bool FP8>
-MfmaFn pick_mode(GemvMode mode, int kh, int bt, int ups) {
+MfmaFn pick_mode(GemvMode mode, int kh, int bt, int ups, bool xb) {
+  if (xb) return mode == kGemvRmsNorm ? pick_xb<kGemvRmsNorm, FP8>(kh)
+                                      : pick_xb<kGemvPlain, FP8>(kh);
   switch (mode) {
     case kGemvRmsNorm: return pick_kh<kGemvRmsNorm, FP8>(kh, bt, ups);
     case kGemvSwiGLU: return pick_kh<kGemvSwiGLU, FP8>(kh, bt, ups);
@@ -400,16 +520,25 @@ hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
   // Spread the groups evenly: every workgroup owns gpw or gpw - 1 groups.
   grid = (a.groups + a.gpw - 1) / a.gpw;
   const int kh = K / 512;
-  const int bt = B >= 9 ? 2 : 1;  // batch column tiles of the 16-row pass
-  const int ups = pick_sets(mode, a.gpw);
-  const MfmaFn fn = w.fp8 ? pick_mode<true>(mode, kh, bt, ups) : pick_mode<false>(mode, kh, bt, ups);
   const int nwm = gemv_is_swiglu(mode) ? 2 : 1;
-  const size_t lds = sizeof(float) * a.gpw * nwm * kWavesM * 8 * bt * kRowsPerGroup;
+  // Above 16 rows one weight matrix takes 32-row passes when the LDS holds
+  // rows 16..31 of x (16 KB x KH) next to the 32-column partial sums; else
+  // 16-row passes, each reading the weights again.
+  const size_t xb_bytes = (size_t)kWavesM * 2 * kh * kWave * 16;
+  const size_t part32 = sizeof(float) * a.gpw * nwm * kWavesM * 32 * kRowsPerGroup;
+  const bool xb = nwm == 1 && B > kBatchTile && xb_bytes + part32 <= 152 * 1024;
+  const int bt = xb || B >= 9 ? 2 : 1;  // batch column tiles held in registers
+  const int pass = xb ? 32 : kBatchTile;
+  const int ups = pick_sets(mode, a.gpw);
+  const MfmaFn fn = w.fp8 ? pick_mode<true>(mode, kh, bt, ups, xb)
+                          : pick_mode<false>(mode, kh, bt, ups, xb);
+  const size_t lds = xb ? xb_bytes + part32
+                        : sizeof(float) * a.gpw * nwm * kWavesM * 8 * bt * kRowsPerGroup;
   if (lds > 48 * 1024) {
     hipError_t e = allow_large_lds(reinterpret_cast<const void*>(fn));
     if (e != hipSuccess) return e;
   }
-  dim3 g(grid, (B + kBatchTile - 1) / kBatchTile);
+  dim3 g(grid, (B + pass - 1) / pass);
   hipLaunchKernelGGL(fn, g, dim3(kThreadsM), lds, stream, a);
   return hipGetLastError();
 }

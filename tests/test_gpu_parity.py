@@ -132,6 +132,10 @@ MFMA_CASES = [
     ("f2", 4, 4096, 14336), ("f2", 32, 4096, 1792), ("f2", 9, 2048, 777),
     ("plain", 16, 4096, 4100), ("plain", 3, 2048, 8), ("f2", 3, 4096, 1000),
     ("f2", 3, 2048, 515),
+    # 32-row passes of one matrix (rows 16..31 of x in LDS): the QKV shape at
+    # B=32, ragged batches, two passes (B=40), K=2048 with more groups
+    ("f1", 32, 4096, 6144), ("plain", 24, 4096, 4096), ("f1", 21, 2048, 1000),
+    ("plain", 40, 2048, 3000), ("plain", 32, 4096, 2040),
 ]
 
 
@@ -268,6 +272,7 @@ FP8_CASES = [
     ("f1", 16, 4096, 6144), ("f1", 32, 2048, 1032), ("f2", 17, 4096, 600),
     ("f2n", 9, 2048, 100), ("plain", 3, 2048, 8), ("plain", 16, 4096, 4100),
     ("f2", 2, 4096, 520), ("f2n", 2, 4096, 1000),
+    ("f1", 32, 4096, 6144), ("plain", 20, 4096, 777), ("f1", 40, 2048, 520),
 ]
 
 
