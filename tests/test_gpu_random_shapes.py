@@ -4,8 +4,9 @@ The hand-picked parity cases cover the decode shapes and known edges; these
 draw the rest of the contract at random: every GEMV mode (plain, F1, F2,
 RMSNorm→F2) in fp16 and e4m3 weights with batches that land on both the
 VALU and the MFMA kernel (K ∈ {2048, 4096} is weighted up so the MFMA path
-is hit), ragged K and N, and F4 over random batch, head grouping, KV length
-and split count.  The draws are fixed by the seed, so every run tests the
+is hit), ragged K and N, one weight matrix at 17..48 rows (the MFMA kernel's
+32-row passes), and F4 over random batch, head grouping, KV length and
+split count.  The draws are fixed by the seed, so every run tests the
 same cases; each prints its case before it runs.  DB_RANDOM_SHAPES=<n> and
 DB_RANDOM_SEED=<s> draw a larger or different set for a one-off sweep (the
 F4 count is half the GEMV count).  Bars as in the parity
@@ -72,6 +73,23 @@ def _gemv_cases(n=N_GEMV, seed=SEED):
     return cases
 
 
+def _pass32_cases(n=max(16, N_GEMV // 3), seed=SEED + 2):
+    """One weight matrix at 17..48 rows with K in {2048, 4096}: the 32-row
+    passes that hold rows 16..31 of x in LDS (and a second pass above 32)."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < n:
+        mode = ("plain", "f1")[rng.integers(2)]
+        dtype = "fp8" if rng.random() < 0.5 else "f16"
+        B = int(rng.choice([17, 20, 24, 25, 31, 32, 33, 40, 48]))
+        K = int(rng.choice([2048, 4096]))
+        N = int(rng.integers(1, 6145))
+        if B * N * K > 8 * MAC_BUDGET:
+            continue
+        cases.append((mode, dtype, B, K, N, int(rng.integers(1 << 30))))
+    return cases
+
+
 def _f4_cases(n=N_GEMV // 2, seed=SEED + 1):
     rng = np.random.default_rng(seed)
     cases = []
@@ -91,7 +109,7 @@ def _lib():
     cref.load()
 
 
-@pytest.mark.parametrize("mode,dtype,B,K,N,seed", _gemv_cases())
+@pytest.mark.parametrize("mode,dtype,B,K,N,seed", _gemv_cases() + _pass32_cases())
 def test_random_gemv_shapes(mode, dtype, B, K, N, seed):
     print(f"[rand-gemv] {mode} {dtype} B={B} K={K} N={N} seed={seed}", flush=True)
     gen = torch.Generator().manual_seed(seed)
