@@ -12,8 +12,8 @@
 //  * Workgroups of one pair are numbered so that they all land on the same
 //    XCD (workgroup i is dispatched to XCD i % 8).
 //  * A wave walks 16-row tiles of its split (tile w, w + NW, ...) with two
-//    register sets of two tiles each, so two to four tiles (16-32 KB) of K
-//    and V are in flight per wave.
+//    register sets of one tile each, so one or two tiles (8-16 KB) of K and
+//    V are in flight per wave.
 //  * Scores for a tile come from four v_mfma_f32_16x16x32_f16: A = the
 //    16 x 128 K tile straight from HBM (16 B per lane per k-step), B = Q^T
 //    with the G query heads as columns (zero-padded to 16).  The accumulator
@@ -58,7 +58,6 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kTile = 16;
-constexpr int kPrefetch = 4;  // tiles loaded up front on the short path
 constexpr int kMergeChunk = 8;
 // Row stride (halves) of a V tile in LDS: 128 + 16 padding keeps the four
 // rows one transposed read touches in different banks.
@@ -223,52 +222,28 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
   };
 
   // ---- stream this wave's tiles ------------------------------------------
-  // Long runs use two register sets of two tiles each.  An iteration loads
-  // set B, consumes set A, reloads A and consumes B, so four tiles are in
-  // flight between consumptions and every wait is for one set only.  (Set B
-  // is loaded and consumed in the same iteration, which keeps the compiler
-  // from draining all loads at the loop header, as it does for a ring whose
-  // slots are consumed before they are reloaded.)
-  if (nt >= 6) {
-    u4 ka[2][4], va[2][4], kb[2][4], vb[2][4];
-    load_tile(ka[0], va[0], first);
-    load_tile(ka[1], va[1], first + NW);
+  // Two register sets of one tile each: an iteration loads set B, consumes
+  // set A, reloads A and consumes B, so one or two tiles are in flight and
+  // every wait is for one tile.  (Set B is loaded and consumed in the same
+  // iteration, which keeps the compiler from draining all loads at the loop
+  // header.)  Measured on MI355X against sets of two tiles (two to four in
+  // flight): 24.5 vs 25.0 us at batch 1, L = 32768, and 1-1.5% faster at
+  // batch 4 and 8; deeper queues per wave only spread the tiles' arrival
+  // times and lengthen the tail of the slowest wave.
+  if (nt > 0) {
+    u4 ka[4], va[4], kb[4], vb[4];
+    load_tile(ka, va, first);
     int k = 0;
-    for (; k + 6 <= nt; k += 4) {
-      load_tile(kb[0], vb[0], first + NW * (k + 2));
-      load_tile(kb[1], vb[1], first + NW * (k + 3));
-      compute_tile(ka[0], va[0], first + NW * k);
-      compute_tile(ka[1], va[1], first + NW * (k + 1));
-      load_tile(ka[0], va[0], first + NW * (k + 4));
-      load_tile(ka[1], va[1], first + NW * (k + 5));
-      compute_tile(kb[0], vb[0], first + NW * (k + 2));
-      compute_tile(kb[1], vb[1], first + NW * (k + 3));
+    for (; k + 3 <= nt; k += 2) {
+      load_tile(kb, vb, first + NW * (k + 1));
+      compute_tile(ka, va, first + NW * k);
+      load_tile(ka, va, first + NW * (k + 2));
+      compute_tile(kb, vb, first + NW * (k + 1));
     }
-    // 2 <= nt - k <= 5 tiles remain; set A holds tiles k and k + 1.
-    if (k + 2 < nt) load_tile(kb[0], vb[0], first + NW * (k + 2));
-    if (k + 3 < nt) load_tile(kb[1], vb[1], first + NW * (k + 3));
-    compute_tile(ka[0], va[0], first + NW * k);
-    compute_tile(ka[1], va[1], first + NW * (k + 1));
-    if (k + 4 < nt) load_tile(ka[0], va[0], first + NW * (k + 4));
-    if (k + 2 < nt) compute_tile(kb[0], vb[0], first + NW * (k + 2));
-    if (k + 3 < nt) compute_tile(kb[1], vb[1], first + NW * (k + 3));
-    if (k + 4 < nt) compute_tile(ka[0], va[0], first + NW * (k + 4));
-  } else {
-    // Fewer than 2 * kPrefetch tiles: load what fits, refill once.
-    u4 kb[kPrefetch][4], vb[kPrefetch][4];
-#pragma unroll
-    for (int s = 0; s < kPrefetch; ++s)
-      if (s < nt) load_tile(kb[s], vb[s], first + NW * s);
-#pragma unroll
-    for (int s = 0; s < kPrefetch; ++s) {
-      if (s < nt) {
-        compute_tile(kb[s], vb[s], first + NW * s);
-        if (s + kPrefetch < nt) load_tile(kb[s], vb[s], first + NW * (s + kPrefetch));
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < kPrefetch; ++s)
-      if (kPrefetch + s < nt) compute_tile(kb[s], vb[s], first + NW * (kPrefetch + s));
+    // One or two tiles remain; set A holds tile k.
+    if (k + 1 < nt) load_tile(kb, vb, first + NW * (k + 1));
+    compute_tile(ka, va, first + NW * k);
+    if (k + 1 < nt) compute_tile(kb, vb, first + NW * (k + 1));
   }
 
   // ---- merge the waves of the workgroup through LDS ---------------------
