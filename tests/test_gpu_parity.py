@@ -368,6 +368,10 @@ F4_CASES = [
     (1, 8, 8, 300, 3), (2, 16, 8, 257, 5), (1, 64, 8, 100, None),
     (1, 32, 8, 1, None), (1, 32, 8, 15, 4), (1, 32, 8, 17, 2), (3, 32, 8, 4097, 7),
     (1, 4, 4, 2000, 256),
+    # Tile-stream edges: with S = 1 each of the 8 waves walks 3 tiles (L = 384), 3-4 with a
+    # partial last tile (391), 4-5 (528) or 5-6 (720) tiles through the two register sets.
+    (1, 32, 8, 384, 1), (1, 32, 8, 391, 1), (1, 32, 8, 528, 1), (1, 32, 8, 720, 1),
+    (2, 32, 8, 1040, 2),
 ]
 
 
