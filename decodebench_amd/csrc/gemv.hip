@@ -93,13 +93,12 @@ hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
   while (U > 1 && (size_t)padded_chunks(U) * 16 > 152 * 1024) U = U >= 7 ? 4 : U / 2;
   a.steps = (a.wchunks + kWave * U - 1) / (kWave * U);
   a.kp8 = padded_chunks(U);
-  const int R = gemv_rows_per_group(mode, w.fp8, U);
-  a.groups = (N + R - 1) / R;
-
   // Batch rows per workgroup pass: as many as the batch and the LDS budget
   // (152 KB of the 160 KB per CU) allow.
   int nb = B >= 8 ? 8 : (B >= 4 ? 4 : (B >= 2 ? 2 : 1));
   while (nb > 1 && (size_t)nb * a.kp8 * 16 > 152 * 1024) nb /= 2;
+  const int R = gemv_rows_per_group(mode, w.fp8, U, nb);
+  a.groups = (N + R - 1) / R;
   const GemvFn fn = w.fp8 ? gemv_pick_fp8(mode, nb, U) : gemv_pick_f16(mode, nb, U);
   const size_t lds = (size_t)nb * a.kp8 * 16;
   if (lds > 48 * 1024) {
