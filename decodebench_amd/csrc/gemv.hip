@@ -44,6 +44,19 @@ int pick_waves(int groups, int cu_count) {
   return waves_for(groups, cu_count * (forced > 0 ? forced : 32));
 }
 
+// fp16 F1 at one batch row with 2 rows per wave instead of 1 (see
+// launch_gemv).
+GemvFn gemv_pick_f1_two_rows(int u) {
+  constexpr int WV = gemv_wg_waves(kGemvRmsNorm, false, 1);
+  switch (u) {
+    case 1: return gemv_kernel<kGemvRmsNorm, 1, 2, 1, false, WV>;
+    case 2: return gemv_kernel<kGemvRmsNorm, 1, 2, 2, false, WV>;
+    case 4: return gemv_kernel<kGemvRmsNorm, 1, 2, 4, false, WV>;
+    case 7: return gemv_kernel<kGemvRmsNorm, 1, 2, 7, false, WV>;
+    default: return gemv_kernel<kGemvRmsNorm, 1, 2, 8, false, WV>;
+  }
+}
+
 }  // namespace
 
 hipError_t allow_large_lds(const void* fn) {
@@ -97,9 +110,18 @@ hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
   // (152 KB of the 160 KB per CU) allow.
   int nb = B >= 8 ? 8 : (B >= 4 ? 4 : (B >= 2 ? 2 : 1));
   while (nb > 1 && (size_t)nb * a.kp8 * 16 > 152 * 1024) nb /= 2;
-  const int R = gemv_rows_per_group(mode, w.fp8, U, nb);
+  int R = gemv_rows_per_group(mode, w.fp8, U, nb);
+  // fp16 F1 at one batch row (8-wave workgroups): 2 rows per wave when that
+  // gives every CU the same number of whole workgroups (N / 16 a multiple of
+  // the CU count), else 1.  Measured at K = 4096: N = 4096 with 2 rows
+  // 6.90 -> 6.77 us (one workgroup per CU); N = 6144 with 2 rows 9.21 ->
+  // 10.18 us (1.5 workgroups per CU).
+  const bool f1_two_rows = !w.fp8 && mode == kGemvRmsNorm && nb == 1 && R == 1 &&
+                           ((N + 15) / 16) % cu_count == 0;
+  if (f1_two_rows) R = 2;
   a.groups = (N + R - 1) / R;
-  const GemvFn fn = w.fp8 ? gemv_pick_fp8(mode, nb, U) : gemv_pick_f16(mode, nb, U);
+  const GemvFn fn = f1_two_rows ? gemv_pick_f1_two_rows(U)
+                               : (w.fp8 ? gemv_pick_fp8(mode, nb, U) : gemv_pick_f16(mode, nb, U));
   const size_t lds = (size_t)nb * a.kp8 * 16;
   if (lds > 48 * 1024) {
     hipError_t e = allow_large_lds(reinterpret_cast<const void*>(fn));
