@@ -2,8 +2,8 @@
 // gfx950, shared by the fp16-weight (gemv.hip) and fp8-weight (gemv_fp8.hip)
 // translation units, which instantiate disjoint halves of it.
 //
-//  * A workgroup is 4 waves (1 for the fp16 gate/up pair and 8 for fp16
-//    F1 at one batch row, see gemv_wg_waves).  The activation rows it needs (x, or the
+//  * A workgroup is 4 waves (1 for the fp16 gate/up pair and 8 for the
+//    other fp16 modes at one batch row, see gemv_wg_waves).  The activation rows it needs (x, or the
 //    RMS-normalised x) are built ONCE per workgroup in LDS; the normalised
 //    vector never goes to HBM.
 //  * Each wave owns groups of R consecutive weight rows and streams them with
@@ -40,15 +40,15 @@ namespace dbk {
 // Waves per workgroup.  Measured on MI355X at K = 4096, one batch row
 // (graph back-to-back, interleaved runs): the fp16 gate/up pair streams
 // fastest with single-wave workgroups, which start and retire independently
-// (F2 35.2 -> 33.9 us, RMSNorm->F2 36.3 -> 35.7 us); fp16 F1 with 8 waves of
-// one row each sharing the norm prologue (F1-QKV 9.51 -> 9.19 us, F1 at
-// N = 4096 unchanged); every other mode, batch and weight type is fastest
-// with 4 waves sharing one activation prologue (single waves cost up to
-// 1.5x on the e4m3 projections and F1).
+// (F2 35.2 -> 33.9 us, RMSNorm->F2 36.3 -> 35.7 us); fp16 F1 and the plain
+// projection with 8 waves sharing one activation prologue (F1-QKV 9.51 ->
+// 9.21 us, F1 6.90 -> 6.75 us, plain [4096, 14336] 19.17 -> 18.45 us,
+// [14336, 4096] 19.18 -> 18.85 us); every other batch and weight type is
+// fastest with 4 waves (single waves cost up to 1.5x on the e4m3
+// projections and F1, 8 waves lose on e4m3 F1).
 constexpr int gemv_wg_waves(int mode, bool fp8, int nb) {
   if (fp8 || nb != 1) return 4;
-  if (gemv_is_swiglu(mode)) return 1;
-  return mode == kGemvRmsNorm ? 8 : 4;
+  return gemv_is_swiglu(mode) ? 1 : 8;
 }
 
 struct GemvArgs {
@@ -80,13 +80,15 @@ hipError_t allow_large_lds(const void* fn);
 
 // Rows per wave group, measured on MI355X at the decode shapes: fp16 keeps
 // 16 loads of 16 bytes per lane per tile (2 rows x 8 chunks, or the gate/up
-// pair x 1 row), except fp16 F1 at one batch row, whose 8-wave workgroups
-// take 1 row per wave (8 KB tiles; 2 rows there, or 1 row at two batch rows,
-// measured slower); e4m3 rows are half as long, and 2 rows per group (8
-// loads for one matrix, 16 for the pair) beat both 1 and 4 rows at K = 4096.
+// pair x 1 row), except F1 and the plain projection at one batch row,
+// whose 8-wave workgroups take 1 row per wave (8 KB tiles; 1 row at two
+// batch rows measured slower; the launcher gives F1 2 rows where that
+// fills every CU with whole workgroups); e4m3 rows are half as long, and 2
+// rows per group (8 loads for one matrix, 16 for the pair) beat both 1 and
+// 4 rows at K = 4096.
 constexpr int gemv_rows_per_group(int mode, bool fp8, int u, int nb) {
   const int nw = gemv_is_swiglu(mode) ? 2 : 1;
-  if (!fp8 && mode == kGemvRmsNorm && nb == 1) return 1;
+  if (!fp8 && nw == 1 && nb == 1) return 1;
   if (!fp8) return nw == 2 ? 1 : 2;
   return u <= 4 ? 2 : (nw == 1 ? 2 : 1);
 }
