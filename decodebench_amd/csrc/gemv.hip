@@ -119,16 +119,20 @@ hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
   const bool f1_two_rows = !w.fp8 && mode == kGemvRmsNorm && nb == 1 && R == 1 &&
                            ((N + 15) / 16) % cu_count == 0;
   if (f1_two_rows) R = 2;
+  const bool fp8_long_rows = w.fp8 && mode == kGemvPlain && nb == 1 && K > 4096;
+  if (fp8_long_rows) R = 1;
   a.groups = (N + R - 1) / R;
-  const GemvFn fn = f1_two_rows ? gemv_pick_f1_two_rows(U)
-                               : (w.fp8 ? gemv_pick_fp8(mode, nb, U) : gemv_pick_f16(mode, nb, U));
+  const GemvFn fn = f1_two_rows     ? gemv_pick_f1_two_rows(U)
+                    : fp8_long_rows ? gemv_pick_fp8_plain_long(U)
+                    : w.fp8         ? gemv_pick_fp8(mode, nb, U)
+                                    : gemv_pick_f16(mode, nb, U);
   const size_t lds = (size_t)nb * a.kp8 * 16;
   if (lds > 48 * 1024) {
     hipError_t e = allow_large_lds(reinterpret_cast<const void*>(fn));
     if (e != hipSuccess) return e;
   }
   const int waves = pick_waves(a.groups, cu_count);
-  const int wv = gemv_wg_waves(mode, w.fp8, nb);
+  const int wv = fp8_long_rows ? kWavesFp8PlainLong : gemv_wg_waves(mode, w.fp8, nb);
   dim3 grid((waves + wv - 1) / wv, (B + nb - 1) / nb);
   hipLaunchKernelGGL(fn, grid, dim3(wv * kWave), lds, stream, a);
   return hipGetLastError();

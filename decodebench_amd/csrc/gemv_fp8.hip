@@ -7,4 +7,14 @@ namespace dbk {
 
 GemvFn gemv_pick_fp8(GemvMode mode, int nb, int u) { return gemv_pick<true>(mode, nb, u); }
 
+GemvFn gemv_pick_fp8_plain_long(int u) {
+  switch (u) {
+    case 1: return gemv_kernel<kGemvPlain, 1, 1, 1, true, kWavesFp8PlainLong>;
+    case 2: return gemv_kernel<kGemvPlain, 1, 1, 2, true, kWavesFp8PlainLong>;
+    case 4: return gemv_kernel<kGemvPlain, 1, 1, 4, true, kWavesFp8PlainLong>;
+    case 7: return gemv_kernel<kGemvPlain, 1, 1, 7, true, kWavesFp8PlainLong>;
+    default: return gemv_kernel<kGemvPlain, 1, 1, 8, true, kWavesFp8PlainLong>;
+  }
+}
+
 }  // namespace dbk

@@ -73,6 +73,13 @@ using GemvFn = void (*)(GemvArgs);
 // Kernel choice per weight type (each defined in its own translation unit).
 GemvFn gemv_pick_f16(GemvMode mode, int nb, int u);
 GemvFn gemv_pick_fp8(GemvMode mode, int nb, int u);
+// The e4m3 plain projection at one batch row with rows longer than 4096:
+// 8-wave workgroups of one row per wave, which share each workgroup's
+// activation fill (K x 2 bytes) among twice the weight bytes (measured:
+// [4096, 14336] 11.80 -> 11.02 us, e4m3 decode layer 53.4 -> 52.6 us; at
+// K = 4096 they cost 0.24 us, so shorter rows keep the default).
+constexpr int kWavesFp8PlainLong = 8;
+GemvFn gemv_pick_fp8_plain_long(int u);
 
 // Raise a kernel's dynamic-LDS limit to 152 KB, once per kernel function
 // (the attribute is per function, not per launch).  Defined in gemv.hip.
