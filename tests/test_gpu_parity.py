@@ -65,6 +65,9 @@ F1_CASES = [
     (1, 4096, 4096, 1 / 64), (1, 4096, 6144, 0.02), (4, 4096, 6144, 0.02),
     (8, 4096, 6144, 0.02), (5, 4096, 512, 0.02), (16, 4096, 1024, 0.02),
     (1, 14336, 4096, 0.01),
+    # one batch row: 2 rows per wave where (N + 15) / 16 fills every CU with whole 8-wave
+    # workgroups (K = 2048, and N = 4095 with a half-empty last group), else 1
+    (1, 2048, 8192, 0.02), (1, 4096, 4095, 1 / 64),
 ]
 
 
@@ -268,6 +271,8 @@ FP8_CASES = [
     ("f2n", 1, 4096, 14336), ("f2n", 5, 4096, 257),
     ("plain", 1, 14336, 4096), ("plain", 1, 4096, 4096), ("plain", 4, 14336, 512),
     ("plain", 1, 16, 5), ("plain", 12, 4096, 300),
+    # rows longer than 4096 at one batch row: 8-wave workgroups of one row per wave
+    ("plain", 1, 4112, 777), ("plain", 1, 6000, 1),
     # batched e4m3 on the MFMA kernel (K in {2048, 4096}, batches from 2 / 3 rows)
     ("f1", 16, 4096, 6144), ("f1", 32, 2048, 1032), ("f2", 17, 4096, 600),
     ("f2n", 9, 2048, 100), ("plain", 3, 2048, 8), ("plain", 16, 4096, 4100),
