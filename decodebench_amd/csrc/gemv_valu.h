@@ -3,9 +3,9 @@
 // translation units, which instantiate disjoint halves of it.
 //
 //  * A workgroup is 4 waves (1 for the fp16 gate/up pair and 8 for the
-//    other fp16 modes at one batch row, see gemv_wg_waves).  The activation rows it needs (x, or the
-//    RMS-normalised x) are built ONCE per workgroup in LDS; the normalised
-//    vector never goes to HBM.
+//    other fp16 modes at one batch row, see gemv_wg_waves).  The
+//    activation rows it needs (x, or the RMS-normalised x) are built ONCE
+//    per workgroup in LDS; the normalised vector never goes to HBM.
 //  * Each wave owns groups of R consecutive weight rows and streams them with
 //    128-bit non-temporal loads: lane l reads the 16-byte chunks l, l+64, ...
 //    of a row, so one load instruction covers 1 KB of contiguous weights.
