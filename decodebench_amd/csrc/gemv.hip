@@ -114,11 +114,21 @@ hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
   // fp16 F1 at one batch row (8-wave workgroups): 2 rows per wave when that
   // gives every CU the same number of whole workgroups (N / 16 a multiple of
   // the CU count), else 1.  Measured at K = 4096: N = 4096 with 2 rows
-  // 6.90 -> 6.75 us (one workgroup per CU); N = 6144 with 2 rows 9.21 ->
+  // 6.90 -> 6.64 us (one workgroup per CU); N = 6144 with 2 rows 9.21 ->
   // 10.18 us (1.5 workgroups per CU).
   const bool f1_two_rows = !w.fp8 && mode == kGemvRmsNorm && nb == 1 && R == 1 &&
                            ((N + 15) / 16) % cu_count == 0;
-  if (f1_two_rows) R = 2;
+  if (f1_two_rows) {
+    R = 2;
+    // Two rows of 4 chunks per lane keep the 8 KB tile of the one-row shape
+    // (F1 at N = 4096: 6.77 -> 6.64 us against 8 chunks).  Fewer chunks per
+    // lane pad the activation row no more, so the LDS size only shrinks.
+    if (U == 8) {
+      U = 4;
+      a.steps = (a.wchunks + kWave * U - 1) / (kWave * U);
+      a.kp8 = padded_chunks(U);
+    }
+  }
   // e4m3 plain projection at one batch row with rows longer than 4096: 8-wave
   // workgroups of one row per wave (see kWavesFp8PlainLong).
   const bool fp8_long_rows = w.fp8 && mode == kGemvPlain && nb == 1 && K > 4096;
