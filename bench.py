@@ -23,7 +23,8 @@ the 256 MB Infinity Cache), so every step streams its weights from HBM.
                  with the per-trial samples and a fused-vs-unfused output
                  check that decodebench_amd.validate reads
   cpu_baseline   the torch CPU restatement of the reference stages
-                 (oracle/stages.py) on this host's cores, F2 at full size
+                 (oracle/stages.py) on this host's cores: F2 at full size
+                 (the headline), with F1 (config 1) and F4 (L = 8192) rows
 
 ``--gpus N`` with N > 1 exits with an error: this build runs on one GPU.
 """
@@ -136,20 +137,30 @@ def time_graph_launches(case, min_launches: int = 96, replays: int = 20):
         samples.append(e0.elapsed_time(e1) * 1e3 / per_graph)
     samples.sort()
     del graph
+    torch.cuda.synchronize()
+    from decodebench_amd import ops
+
+    ops.release_captured_workspaces()
     return samples[len(samples) // 2], per_graph
 
 
+CHECK_REL_L2 = 1e-2
+
+
 def check_case(case) -> float:
-    """Fused output vs the unfused torch stages on the GPU (rtol/atol 1e-2)."""
+    """Fused output vs the unfused torch stages on the GPU: rtol/atol 1e-2
+    elementwise, and relative L2 <= 1e-2, which an all-zero output fails
+    also where |o| is below atol (F4 at long KV lengths)."""
     import torch
 
     ref = case.seq._replay_body(case.inputs).float()
     out = case.fused(case.inputs).float()
     torch.cuda.synchronize()
-    if not torch.allclose(out, ref, rtol=1e-2, atol=1e-2):
+    err = float((out - ref).norm() / ref.norm().clamp_min(1e-30))
+    if not torch.allclose(out, ref, rtol=1e-2, atol=1e-2) or not err <= CHECK_REL_L2:
         raise RuntimeError(f"{case.name}: fused output differs from the torch stages "
-                           f"(max abs {float((out - ref).abs().max()):.3e})")
-    return float((out - ref).norm() / ref.norm().clamp_min(1e-30))
+                           f"(max abs {float((out - ref).abs().max()):.3e}, rel-L2 {err:.3e})")
+    return err
 
 
 def fused_check(case) -> dict:
@@ -245,8 +256,8 @@ def kernels_per_call(kw: dict) -> int:
 
 def f4_partial_bytes(kw: dict, batch: int = 1) -> int:
     """HBM bytes a fused F4 call adds over a single-pass kernel: the split
-    partial records (o, m, l per head and split) written by the first launch
-    and read back by the merge."""
+    partial records (o, m, l per head and split, fp32) written by the first
+    launch and read back by the merge."""
     from decodebench_amd import ops
     from decodebench_amd.demos.llama_decode import LAYER
 
@@ -327,48 +338,94 @@ def load_traffic(path: str) -> dict:
 
 
 # ------------------------------------------------------------ CPU baseline
-def cpu_baseline(seconds: float, replicas: int = 3) -> dict:
-    """F2 (config 2, B = 1) through the torch CPU stages, time-bounded.
+def _cpu_model() -> str:
+    name = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return name
 
-    Calls rotate over ``replicas`` weight copies (705 MB at 3) so the sample
-    is not served from a large host L3."""
+
+def cpu_threads() -> int:
+    """Threads for the CPU baseline: every CPU this process may run on, capped
+    by OMP_NUM_THREADS when the host sets it (the GPU box's CPU share)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def _time_cpu(fn, reps: list, seconds: float) -> tuple[float, int]:
+    """Median seconds per call of fn(*reps[i % n]) over about ``seconds``."""
+    fn(*reps[0])  # warm-up
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        args = reps[len(times) % len(reps)]
+        t0 = time.perf_counter()
+        fn(*args)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """The torch CPU restatement of the reference stages (oracle/stages.py),
+    time-bounded, on this host's cores: F2 (config 2, B = 1, the headline
+    workload; ``seconds``), and beside it F1 (config 1) and F4 (config 4,
+    L = 8192), a third of ``seconds`` each.  Calls rotate over replicas of the
+    large operands (F2: 3, 705 MB) so the sample is not served from a large
+    host L3."""
     import torch
 
     from oracle import stages
 
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
     gen = torch.Generator().manual_seed(42)
     K, N = 4096, 14336
     x = torch.randn(1, K, generator=gen).half()
     Wg = (torch.randn(N, K, generator=gen) * 0.02).half()
     Wu = (torch.randn(N, K, generator=gen) * 0.02).half()
-    reps = [(Wg, Wu)] + [(Wg.clone(), Wu.clone()) for _ in range(replicas - 1)]
-    nbytes = 2 * N * K * 2 + (K + N) * 2
-    stages.f2(x, Wg, Wu)  # warm-up
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 3:
-        wg, wu = reps[len(times) % replicas]
-        t0 = time.perf_counter()
-        stages.f2(x, wg, wu)
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
-    cpu_model = platform.processor() or ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
-    return {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s",
-            "cores": torch.get_num_threads(), "kind": "port",
-            "sample": (f"F2 B=1 Wg/Wu[14336,4096] fp16 via oracle/stages.py (torch CPU), "
-                       f"{len(times)} calls over {replicas} weight replicas in "
-                       f"~{seconds:.0f} s, median {med * 1e6:.0f} us/call"),
-            "us_per_call": round(med * 1e6, 1), "cpu_model": cpu_model,
-            "os_cpu_count": os.cpu_count()}
+    f2_reps = [(x, Wg, Wu)] + [(x, Wg.clone(), Wu.clone()) for _ in range(2)]
+    f2_bytes = 2 * N * K * 2 + (K + N) * 2
+    med, calls = _time_cpu(stages.f2, f2_reps, seconds)
+    del f2_reps, Wg, Wu
+    out = {"value": round(f2_bytes / med / 1e9, 2), "unit": "GB/s", "cores": threads,
+           "kind": "port",
+           "sample": (f"F2 B=1 Wg/Wu[14336,4096] fp16 via oracle/stages.py (torch CPU, "
+                      f"{threads} threads), {calls} calls over 3 weight replicas in "
+                      f"~{seconds:.0f} s, median {med * 1e6:.0f} us/call"),
+           "us_per_call": round(med * 1e6, 1), "cpu_model": _cpu_model(),
+           "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads()}
+
+    rows = {}
+    W = (torch.randn(4096, K, generator=gen) / 64).half()
+    g = (torch.randn(K, generator=gen) * 0.1 + 1).half()
+    f1_reps = [(x, g, W)] + [(x, g, W.clone()) for _ in range(7)]
+    med, calls = _time_cpu(stages.f1, f1_reps, seconds / 3)
+    nb = 4096 * K * 2 + K * 2 + (K + 4096) * 2
+    rows["f1_cfg1"] = {"us_per_call": round(med * 1e6, 1), "GB/s": round(nb / med / 1e9, 2),
+                       "calls": calls, "replicas": len(f1_reps)}
+    del f1_reps, W
+    L = 8192
+    q = torch.randn(1, 32, 128, generator=gen).half()
+    f4_reps = [(q, torch.randn(1, 8, L, 128, generator=gen).half(),
+                torch.randn(1, 8, L, 128, generator=gen).half()) for _ in range(4)]
+    med, calls = _time_cpu(lambda q_, k_, v_: stages.f4(q_, k_, v_), f4_reps, seconds / 3)
+    nb = 2 * 8 * L * 128 * 2 + 2 * 32 * 128 * 2
+    rows["f4_L8192"] = {"us_per_call": round(med * 1e6, 1), "GB/s": round(nb / med / 1e9, 2),
+                        "calls": calls, "replicas": len(f4_reps)}
+    out["rows"] = rows
+    return out
 
 
 # -------------------------------------------------------------------- main
@@ -477,8 +534,9 @@ def main(argv=None) -> int:
 
         # ---- CPU baseline ------------------------------------------------
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
-        log(f"cpu baseline: {out['cpu_baseline']['value']} GB/s on "
-            f"{out['cpu_baseline']['cores']} threads")
+        cb = out["cpu_baseline"]
+        log(f"cpu baseline: F2 {cb['value']} GB/s on {cb['cores']} threads; "
+            + "; ".join(f"{k} {v['us_per_call']} us" for k, v in cb["rows"].items()))
     print(json.dumps(out), flush=True)
     return 0
 

@@ -21,6 +21,11 @@ The counterpart of the reference's ``calibrate`` harness
 The printed lines follow calibrate.cu's output ("t_launch_stream: ... us",
 "G2: PASS"), with the vendor line labelled by the library that ran.
 
+:func:`stream_floor` has no counterpart in the reference either: it times the
+library's read-only streaming probe (``db_stream_read``) at the byte counts
+of the fused batch-1 calls, giving the best time any single launch of that
+size reaches here.
+
 One comparison has no counterpart in the reference: :func:`vendor_f4` times
 F4 (``db_f4_splitkv``) against torch's ``scaled_dot_product_attention`` at
 the benchmark's decode shape (32 query heads, 8 KV heads, head dim 128, fp16,
@@ -128,6 +133,10 @@ def _graph_us(fn, args: list, min_launches: int = 48, replays: int = 10) -> floa
         torch.cuda.synchronize()
         samples.append(e0.elapsed_time(e1) * 1e3 / per_graph)
     del graph
+    torch.cuda.synchronize()
+    from decodebench_amd import ops
+
+    ops.release_captured_workspaces()
     samples.sort()
     return samples[len(samples) // 2]
 
@@ -209,6 +218,77 @@ def null_launch(iters: int = 500) -> NullLaunch:
     torch.cuda.synchronize()
     t_in_graph = e0.elapsed_time(e1) * 1e3 / iters
     return NullLaunch(t_stream, t_graph, t_in_graph)
+
+
+# Byte counts of the fused batch-1 calls (the algorithmic bytes of F4 at L = 1024,
+# e4m3 F1, F1, F4 at L = 8192, F1-QKV, F4 at L = 32768 and F2), each rounded up to
+# whole 16 KB chunks so every probe shape reads the same bytes.
+FLOOR_SIZES = (4_210_688, 16_818_176, 33_579_008, 33_570_816, 50_360_320, 134_234_112,
+               234_917_888)
+
+
+@dataclass
+class StreamFloor:
+    rows: list            # (bytes, {kb_per_wave: us}) per size
+    replicas: dict        # bytes -> replicas rotated through
+    fit_us: float         # fixed cost a of t = a + bytes / bw over the best time per size
+    fit_gbs: float        # bw
+
+    def best_us(self, nbytes: int) -> float:
+        return min(dict(self.rows)[nbytes].values())
+
+    def render(self) -> str:
+        kbs = sorted(self.rows[0][1])
+        head = " | ".join(f"{k} KB/wave us" for k in kbs)
+        out = [f"| bytes | {head} | best GB/s | % of 8 TB/s | 70% bar us | replicas |",
+               "|---|" + "---|" * (len(kbs) + 4)]
+        for nbytes, per in self.rows:
+            best = min(per.values())
+            gbs = nbytes / (best * 1e3)
+            out.append(f"| {nbytes:,} | " + " | ".join(f"{per[k]:.2f}" for k in kbs) +
+                       f" | {gbs:.0f} | {gbs / 80:.1f} | {nbytes / 8e12 / 0.7 * 1e6:.2f} | "
+                       f"{self.replicas[nbytes]} |")
+        out.append(f"floor fit: t = {self.fit_us:.2f} us + bytes / {self.fit_gbs:.0f} GB/s")
+        return "\n".join(out)
+
+
+def stream_floor(sizes=FLOOR_SIZES, kbs=(4, 8, 16), min_launches: int = 96,
+                 replays: int = 10) -> StreamFloor:
+    """Single-launch streaming floor: ``db_stream_read`` (a read-only kernel
+    of 16-byte non-temporal loads, each wave one contiguous chunk of
+    ``kb`` KB) timed back to back in a hipGraph over zero-filled buffers
+    rotated through a working set of at least 2 x (8 x 4 MB L2 + 256 MB
+    Infinity Cache), for each byte count in ``sizes``.  A fused kernel that
+    reads the same bytes in one launch cannot beat the best of these."""
+    import torch
+
+    from decodebench_amd import ops
+
+    ops.load_library()
+    chunk = 16 * 1024
+    working_set = 2 * (8 * 4 + 256) * 2**20
+    rows, reps = [], {}
+    sink = None
+    for nbytes in sizes:
+        padded = -(-nbytes // chunk) * chunk
+        n = max(2, -(-working_set // padded))
+        bufs = [torch.zeros(padded, dtype=torch.uint8, device="cuda") for _ in range(n)]
+        if sink is None or sink.numel() < padded // 16:
+            sink = torch.empty(padded // 16, dtype=torch.int32, device="cuda")
+        per = {}
+        for kb in kbs:
+            per[kb] = _graph_us(lambda b, kb=kb: ops.stream_read(b, kb, sink), bufs,
+                                min_launches=min_launches, replays=replays)
+        rows.append((nbytes, per))
+        reps[nbytes] = n
+        del bufs
+        torch.cuda.empty_cache()
+    xs = [nb for nb, _ in rows]
+    ys = [min(per.values()) for _, per in rows]
+    mx, my = sum(xs) / len(xs), sum(ys) / len(ys)
+    slope = sum((x - mx) * (y - my) for x, y in zip(xs, ys)) / sum((x - mx) ** 2 for x in xs)
+    return StreamFloor(rows=rows, replicas=reps, fit_us=my - slope * mx,
+                       fit_gbs=1.0 / slope / 1e3)
 
 
 def _vendor_name() -> str:

@@ -26,74 +26,81 @@ from __future__ import annotations
 
 import argparse
 import csv
-import importlib.util
 import os
+import runpy
 import sys
 
 from decodebench_amd.verdict import DEFAULT_BYTE_THRESHOLD
 
 
-def parse_comma_list(s: str) -> list[int]:
-    try:
-        return [int(x.strip()) for x in s.split(",") if x.strip()]
-    except Exception:
-        raise argparse.ArgumentTypeError(f"Invalid comma-separated list: '{s}'")
+def _int_list(text: str) -> list[int]:
+    """``"1,2,4"`` -> ``[1, 2, 4]``; anything else is an argparse error."""
+    items = [part.strip() for part in text.split(",")]
+    if not items or not all(part.lstrip("-").isdigit() for part in items if part):
+        raise argparse.ArgumentTypeError(f"expected integers separated by commas, got {text!r}")
+    return [int(part) for part in items if part]
 
 
 def build_parser() -> argparse.ArgumentParser:
     parser = argparse.ArgumentParser(
         prog="decodebench",
-        description=("DecodeBench: compare launch overhead with an analytic eliminable-byte "
-                     "estimate in LLM decode fusion."))
+        description=("Split a decode-chain fusion gain into launch overhead (stream vs graph "
+                     "replay) and an analytic estimate of the intermediate bytes it removes."))
     sub = parser.add_subparsers(dest="command", required=True)
 
-    demo_p = sub.add_parser("demo", help="Run a bundled Llama-decode demo.")
-    demo_p.add_argument("name", choices=["f1", "f2", "f4"], help="Demo name.")
+    def timing_opts(p, threshold=True):
+        p.add_argument("--trials", type=int, default=30, help="timed trials per variant")
+        if threshold:
+            p.add_argument("--byte-threshold", type=float, default=DEFAULT_BYTE_THRESHOLD,
+                           help="eliminable/total byte ratio above which bytes are material")
+        p.add_argument("--dry-run", action="store_true",
+                       help="print what would run, touch no GPU")
+
+    demo_p = sub.add_parser("demo", help="profile one of the Llama-shaped decode demos")
+    demo_p.add_argument("name", choices=["f1", "f2", "f4"],
+                        help="f1 RMSNorm->GEMV, f2 gate/up+SwiGLU, f4 attention")
     demo_p.add_argument("--dim", type=int, choices=[2048, 4096], default=4096,
-                        help="Hidden dimension.")
-    demo_p.add_argument("--batch", type=int, default=1, help="Batch size.")
-    demo_p.add_argument("--trials", type=int, default=30, help="Number of timing trials.")
-    demo_p.add_argument("--byte-threshold", type=float, default=DEFAULT_BYTE_THRESHOLD,
-                        help="Byte ratio threshold.")
-    demo_p.add_argument("--csv", type=str, help="Output path for trial CSV.")
-    demo_p.add_argument("--dry-run", action="store_true", help="Print plan and exit.")
+                        help="model width")
+    demo_p.add_argument("--batch", type=int, default=1, help="decode batch rows")
+    timing_opts(demo_p)
+    demo_p.add_argument("--csv", type=str, help="write every trial to this CSV file")
     demo_p.add_argument("--fused", action="store_true",
-                        help="Also time the HIP fused kernel of this demo.")
+                        help="add this library's HIP kernel as the fused variant")
 
-    prof_p = sub.add_parser("profile", help="Profile a user-defined Sequence chain.")
-    prof_p.add_argument("target", help="Target sequence wrapper (path/to/module.py:build_fn).")
-    prof_p.add_argument("--trials", type=int, default=30, help="Number of timing trials.")
-    prof_p.add_argument("--byte-threshold", type=float, default=DEFAULT_BYTE_THRESHOLD,
-                        help="Byte ratio threshold.")
-    prof_p.add_argument("--csv", type=str, help="Output path for trial CSV.")
-    prof_p.add_argument("--dry-run", action="store_true", help="Print plan and exit.")
+    prof_p = sub.add_parser("profile", help="profile a Sequence built by your own script")
+    prof_p.add_argument("target", help="FILE.py:FUNCTION returning (sequence, inputs)")
+    timing_opts(prof_p)
+    prof_p.add_argument("--csv", type=str, help="write every trial to this CSV file")
 
-    sweep_p = sub.add_parser("sweep", help="Sweep batch sizes and hidden dims for a demo.")
-    sweep_p.add_argument("name", choices=["f1", "f2", "f4"], help="Demo name.")
-    sweep_p.add_argument("--batch", type=parse_comma_list, default=[1, 2, 4, 8],
-                         help="Comma-separated batch sizes to sweep.")
+    sweep_p = sub.add_parser("sweep", help="profile a demo over several batch sizes")
+    sweep_p.add_argument("name", choices=["f1", "f2", "f4"],
+                         help="f1 RMSNorm->GEMV, f2 gate/up+SwiGLU, f4 attention")
+    sweep_p.add_argument("--batch", type=_int_list, default=[1, 2, 4, 8],
+                         help="batch sizes, e.g. 1,2,4,8")
     sweep_p.add_argument("--dim", type=int, choices=[2048, 4096], default=4096,
-                         help="Hidden dimension.")
-    sweep_p.add_argument("--trials", type=int, default=30, help="Number of timing trials.")
-    sweep_p.add_argument("--csv", type=str, help="Output path for sweep summary CSV.")
-    sweep_p.add_argument("--dry-run", action="store_true", help="Print plan and exit.")
+                         help="model width")
+    timing_opts(sweep_p, threshold=False)
+    sweep_p.add_argument("--csv", type=str, help="write one summary row per batch to this CSV")
     sweep_p.add_argument("--fused", action="store_true",
-                         help="Also time the HIP fused kernel of this demo.")
+                         help="add this library's HIP kernel as the fused variant")
 
-    cal_p = sub.add_parser("calibrate", help="Launch-overhead and GEMV-vs-BLAS calibration.")
+    cal_p = sub.add_parser("calibrate", help="launch-cost and bandwidth calibration")
     cal_p.add_argument("--null", action="store_true",
-                       help="Measure launch overhead (stream and graph).")
+                       help="cost of an empty launch, eager and replayed from a graph")
     cal_p.add_argument("--gate-g2", action="store_true",
-                       help="Compare the fp16 GEMV with the vendor BLAS (G2 gate).")
+                       help="fp16 GEMV bandwidth against the vendor BLAS (G2 gate)")
+    cal_p.add_argument("--stream-floor", action="store_true",
+                       help="single-launch streaming floor: bytes read by one launch vs time")
     cal_p.add_argument("--iters", type=int, default=None,
-                       help="Launches per measurement (default 500 null, 200 GEMV).")
+                       help="launches per measurement (default: 500 empty, 200 GEMV)")
     cal_p.add_argument("--no-rotate", action="store_true",
-                       help="G2 on one weight matrix, as the reference (cache-resident here).")
+                       help="G2 on a single weight copy (it then stays in the caches)")
     cal_p.add_argument("--vendor-f4", action="store_true",
-                       help="Compare F4 with torch scaled_dot_product_attention.")
-    cal_p.add_argument("--kv-len", type=int, default=8192, help="KV length for --vendor-f4.")
-    cal_p.add_argument("--kv-batch", type=int, default=1, help="Batch for --vendor-f4.")
-    cal_p.add_argument("--dry-run", action="store_true", help="Print plan and exit.")
+                       help="F4 against torch scaled_dot_product_attention")
+    cal_p.add_argument("--kv-len", type=int, default=8192, help="KV length for --vendor-f4")
+    cal_p.add_argument("--kv-batch", type=int, default=1, help="batch for --vendor-f4")
+    cal_p.add_argument("--dry-run", action="store_true",
+                       help="print what would run, touch no GPU")
     return parser
 
 
@@ -135,6 +142,15 @@ def _demo(args) -> int:
     return _print_report(report, args.csv)
 
 
+def _load_target(path: str, name: str):
+    """Execute the user's file as a script module and return its ``name``."""
+    namespace = runpy.run_path(path, run_name="decodebench_target")
+    fn = namespace.get(name)
+    if not callable(fn):
+        raise AttributeError(f"{path} defines no function {name!r}")
+    return fn
+
+
 def _profile(args) -> int:
     if ":" not in args.target:
         print("Error: Target must be in the format 'path/to/module.py:build_fn'", file=sys.stderr)
@@ -148,13 +164,8 @@ def _profile(args) -> int:
         print(f"Error: Module path '{module_path}' does not exist.", file=sys.stderr)
         return 1
     try:
-        spec = importlib.util.spec_from_file_location("user_module", module_path)
-        if spec is None or spec.loader is None:
-            raise ImportError(f"Cannot load module from {module_path}")
-        module = importlib.util.module_from_spec(spec)
-        spec.loader.exec_module(module)
-        build_fn = getattr(module, build_fn_name)
-    except Exception as e:
+        build_fn = _load_target(module_path, build_fn_name)
+    except Exception as e:  # report any failure of the user's file, then stop
         print(f"Error loading target: {e}", file=sys.stderr)
         return 1
     if not _gpu_or_error():
@@ -207,8 +218,9 @@ def _sweep(args) -> int:
 
 
 def _calibrate(args) -> int:
-    if not (args.null or args.gate_g2 or args.vendor_f4):
-        print("Error: calibrate needs --null, --gate-g2 and/or --vendor-f4", file=sys.stderr)
+    if not (args.null or args.gate_g2 or args.vendor_f4 or args.stream_floor):
+        print("Error: calibrate needs --null, --gate-g2, --stream-floor and/or --vendor-f4",
+              file=sys.stderr)
         return 2
     if args.iters is not None and args.iters < 1:
         print("Error: --iters must be >= 1", file=sys.stderr)
@@ -218,6 +230,7 @@ def _calibrate(args) -> int:
         return 2
     if args.dry_run:
         what = [w for w, on in (("null", args.null), ("gate-g2", args.gate_g2),
+                                ("stream-floor", args.stream_floor),
                                 ("vendor-f4", args.vendor_f4)) if on]
         print(f"[dry-run] calibrate {' '.join(what)} with iters={args.iters or 'default'}, "
               f"rotate={not args.no_rotate}"
@@ -237,6 +250,8 @@ def _calibrate(args) -> int:
             print(f"Error: GEMV output differs from the vendor BLAS by {g2.max_abs_diff:.3e}",
                   file=sys.stderr)
             rc = 1
+    if args.stream_floor:
+        print(calibrate.stream_floor().render())
     if args.vendor_f4:
         v = calibrate.vendor_f4(L=args.kv_len, B=args.kv_batch)
         print(v.render())

@@ -206,10 +206,13 @@ size_t db_f4_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S) {
   return dbk::f4_workspace_bytes(B, Hq, Hkv, S, D);
 }
 
-int db_f4_splitkv(const void* q, const void* k, const void* v, void* o,
-                  void* ws, size_t ws_bytes, int B, int Hq, int Hkv, int L,
-                  int D, int S, float scale, void* stream) {
-  const char* fn = "db_f4_splitkv";
+}  // extern "C"
+
+namespace {
+
+// Argument contract shared by the F4 entry points (workspace aside).
+int check_f4(const char* fn, const void* q, const void* k, const void* v, const void* o,
+             int B, int Hq, int Hkv, int L, int D, int S, float scale) {
   if (!q || !k || !v || !o) return fail(DB_ERR_INVALID, "%s: null tensor pointer", fn);
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
     return fail(DB_ERR_INVALID, "%s: tensors must be 16-byte aligned", fn);
@@ -227,8 +230,26 @@ int db_f4_splitkv(const void* q, const void* k, const void* v, void* o,
   if (!isfinite(scale)) return fail(DB_ERR_INVALID, "%s: scale must be finite", fn);
   if ((size_t)B * Hkv * L * D >= ((size_t)1 << 40))
     return fail(DB_ERR_INVALID, "%s: KV cache too large", fn);
+  return DB_OK;
+}
+
+// Splits a call actually runs: never more than the 16-row tiles of L.
+int f4_effective_splits(int L, int S) {
   const int ntiles = (L + 15) / 16;
-  const int s_eff = S < ntiles ? S : ntiles;
+  return S < ntiles ? S : ntiles;
+}
+
+}  // namespace
+
+extern "C" {
+
+int db_f4_splitkv(const void* q, const void* k, const void* v, void* o,
+                  void* ws, size_t ws_bytes, int B, int Hq, int Hkv, int L,
+                  int D, int S, float scale, void* stream) {
+  const char* fn = "db_f4_splitkv";
+  const int rc = check_f4(fn, q, k, v, o, B, Hq, Hkv, L, D, S, scale);
+  if (rc) return rc;
+  const int s_eff = f4_effective_splits(L, S);
   if (s_eff > 1) {
     const size_t need = dbk::f4_workspace_bytes(B, Hq, Hkv, S, D);
     if (!ws) return fail(DB_ERR_INVALID, "%s: S=%d needs a workspace", fn, S);
@@ -240,6 +261,35 @@ int db_f4_splitkv(const void* q, const void* k, const void* v, void* o,
   return hip_status(dbk::launch_f4(q, k, v, o, ws, B, Hq, Hkv, L, D, S, scale,
                                    (hipStream_t)stream),
                     fn);
+}
+
+int db_stream_read(const void* src, size_t bytes, int kb_per_wave, unsigned magic,
+                   unsigned* sink, void* stream) {
+  const char* fn = "db_stream_read";
+  if (!src || !sink) return fail(DB_ERR_INVALID, "%s: null pointer", fn);
+  if (!aligned16(src) || !aligned16(sink))
+    return fail(DB_ERR_INVALID, "%s: src and sink must be 16-byte aligned", fn);
+  if (kb_per_wave != 4 && kb_per_wave != 8 && kb_per_wave != 16)
+    return fail(DB_ERR_INVALID, "%s: kb_per_wave=%d not in {4, 8, 16}", fn, kb_per_wave);
+  const size_t chunk = (size_t)kb_per_wave * 1024;
+  if (bytes == 0 || bytes % chunk)
+    return fail(DB_ERR_INVALID, "%s: bytes=%zu is not a positive multiple of %zu", fn, bytes,
+                chunk);
+  if (bytes / chunk > ((size_t)1 << 31))
+    return fail(DB_ERR_INVALID, "%s: bytes=%zu is too large", fn, bytes);
+  return hip_status(dbk::launch_stream_read(src, bytes, kb_per_wave, magic, sink,
+                                            (hipStream_t)stream),
+                    fn);
+}
+
+int db_stream_capture_id(void* stream, unsigned long long* capture_id) {
+  if (!capture_id) return fail(DB_ERR_INVALID, "db_stream_capture_id: null output");
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  unsigned long long id = 0;
+  const hipError_t e = hipStreamGetCaptureInfo((hipStream_t)stream, &status, &id);
+  if (e != hipSuccess) return hip_status(e, "db_stream_capture_id");
+  *capture_id = status == hipStreamCaptureStatusActive ? id : 0;
+  return ok();
 }
 
 int db_null_kernel(void* stream) {
@@ -267,6 +317,10 @@ int db_tune(const char* key, int value) {
     if (value != 0 && value != 1)
       return fail(DB_ERR_INVALID, "db_tune: f4_merge must be 0 or 1");
     t.f4_merge = value;
+  } else if (!strcmp(key, "f4_line")) {
+    if (value < 0 || value > 2)
+      return fail(DB_ERR_INVALID, "db_tune: f4_line must be 0 (auto), 1 (whole lines) or 2");
+    t.f4_line = value;
   } else if (!strcmp(key, "f4_min_tiles")) {
     if (value < 1) return fail(DB_ERR_INVALID, "db_tune: f4_min_tiles must be >= 1");
     t.f4_min_tiles = value;

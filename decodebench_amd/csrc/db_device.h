@@ -61,6 +61,7 @@ constexpr int kQuadSwap1 = 0xB1;      // quad_perm [1,0,3,2]
 constexpr int kQuadSwap2 = 0x4E;      // quad_perm [2,3,0,1]
 constexpr int kRowHalfMirror = 0x141;
 constexpr int kRowMirror = 0x140;
+constexpr int kRowRor8 = 0x128;      // row_ror:8: lane n of a row <- lane (n + 8) % 16
 constexpr int kRowNewBcast0 = 0x150;  // + n: lane n of each row -> whole row
 
 template <int CTRL>

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 
+#include "decodebench_hip.h"
+
 namespace dbk {
 
 // Launch geometry knobs; defaults are the tuned MI355X values.  They can be
@@ -14,9 +16,10 @@ struct Tuning {
                                // (0: 3 for one weight matrix, 4 for the
                                // gate/up pair -- the measured crossovers)
   int f4_blocks_per_cu = 1;    // target F4 workgroups per CU
-  int f4_min_tiles = 2;        // minimum 16-row tiles per F4 split
+  int f4_min_tiles = 8;        // minimum 16-row tiles per F4 split
   int f4_waves = 0;            // waves per F4 workgroup (4 or 8; 0: auto)
   int f4_merge = 0;            // 0: merge splits in a second launch; 1: same launch
+  int f4_line = 0;             // F4 score layout: 0 auto, 1 whole-line K loads, 2 plain
 };
 Tuning& tuning();
 
@@ -68,8 +71,18 @@ hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
 // Split-KV GQA decode attention with the log-sum-exp combine in-kernel.
 size_t f4_workspace_bytes(int B, int Hq, int Hkv, int S, int D);
 int f4_choose_splits(int B, int Hkv, int L, int cu_count);
+// allow_fused_merge = false keeps the merge in the second launch whatever
+// db_tune("f4_merge") says, so the workspace tickets are never read.
 hipError_t launch_f4(const void* q, const void* k, const void* v, void* o,
                      void* ws, int B, int Hq, int Hkv, int L, int D, int S,
-                     float scale, hipStream_t stream);
+                     float scale, hipStream_t stream, bool allow_fused_merge = true);
+
+
+// Read-only streaming probe (stream_probe.hip): `bytes` (a multiple of
+// kb_per_wave KB, kb_per_wave in {4, 8, 16}) read once, kb_per_wave KB per
+// wave; sink needs bytes / 16 words and is written only when the folded
+// data equals `magic`.
+hipError_t launch_stream_read(const void* src, size_t bytes, int kb_per_wave, unsigned magic,
+                              unsigned* sink, hipStream_t stream);
 
 }  // namespace dbk

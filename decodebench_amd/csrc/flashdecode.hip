@@ -15,9 +15,12 @@
 //    register sets of one tile each, so one or two tiles (8-16 KB) of K and
 //    V are in flight per wave.
 //  * Scores for a tile come from four v_mfma_f32_16x16x32_f16: A = the
-//    16 x 128 K tile straight from HBM (16 B per lane per k-step), B = Q^T
-//    with the G query heads as columns (zero-padded to 16).  The accumulator
-//    lands as S[key 4g+i][head n] in lane 16g+n, register i.
+//    K tile straight from HBM, B = Q^T with the G query heads as columns.
+//    The operands split each 128-byte line into its even and odd 16-byte
+//    chunks (even A rows / B columns 0-7 take the even ones), so every K
+//    load instruction reads 8 keys x one whole line; one DPP row rotation
+//    folds the two halves of each score, which land in the same 16-lane
+//    row of the accumulator.
 //  * Online softmax runs in base 2 (scale * log2 e folded into the scores) on
 //    the 4 keys each lane holds; the tile max crosses rows with two lane
 //    swaps.  The fp16 probabilities are already the B operand (P^T) of the
@@ -75,7 +78,7 @@ struct F4Args {
   _Float16* o;         // [B, Hq, D]
   unsigned* ticket;    // [B * Hkv]          split tickets (zero between calls)
   float2* ml;          // [B * Hkv, G, S]    (max, exp-sum) per split, base 2
-  float* opart;        // [B * Hkv, S, G, D] unnormalised outputs
+  float* opart;        // [B * Hkv, S, G, D] unnormalised split outputs
   int fused_merge;     // 1: the last split of a pair merges in this launch
   int B, Hq, Hkv, L, S;
   int ntiles;          // ceil(L / 16)
@@ -103,7 +106,7 @@ __device__ __forceinline__ void store_coherent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int G, int NW>
+template <int G, int NW, bool LINE>
 __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
   static_assert(G >= 1 && G <= 8, "query heads per KV head");
   constexpr int kThreads = NW * kWave;
@@ -134,14 +137,54 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
   const _Float16* Vp = a.v + kv_base;
   const size_t q_base = ((size_t)b * a.Hq + (size_t)kvh * G) * kD;
 
-  // B operand (Q^T): lane (g4, n16) holds q[head n16][d chunk g4 + 4t].
-  h8 qop[4];
+  // Score operands: A = K (keys as rows), B = Q^T (heads as columns); a
+  // 16-byte "chunk" c of a K or q row is its halves 8c..8c+7.  Two layouts:
+  //
+  //  LINE (whole-line K loads): one K load instruction reads 8 keys x one
+  //   128-byte line (line t = chunks 8t..8t+7).  A (key group kg = keys
+  //   8kg..8kg+7): lane (g4, n16), the A row m = n16, holds K[key 8kg +
+  //   (n16 >> 1)][chunk 8t + 2 g4 + (n16 & 1)]: row 2j carries the even
+  //   chunks of key j, row 2j + 1 the odd ones.  B: lane (g4, n16), column
+  //   n16, holds q[head n16 & 7][chunk 8t + 2 g4 + (n16 >> 3)] (zero for
+  //   heads >= G): columns 0-7 pair with the even chunks, 8-15 with the odd
+  //   ones.  Over the two lines the score of key j and head h < 8 is
+  //   D[2j][h] + D[2j + 1][h + 8]; both terms sit in the same 16-lane row of
+  //   the accumulator (registers 2r and 2r + 1, lanes h and h + 8), so one
+  //   DPP row rotation folds them; the other accumulator entries are
+  //   discarded.
+  //  Plain: one K load instruction reads 16 keys x 64 bytes.  A: lane
+  //   (g4, n16) holds K[key n16][chunk g4 + 4t]; B: q[head n16][chunk
+  //   g4 + 4t] (zero for heads >= G); the accumulator is the score matrix.
+  //
+  // Measured on MI355X (32 q / 8 kv heads, graph back-to-back): whole lines
+  // are faster at batch 1 (L = 8192 10.75 -> 10.53 us, L = 32768 24.43 ->
+  // 24.21 us) and wherever a wave walks 1-2 tiles (batch 4 and 8 at
+  // L = 1024: 0.2-0.4 us), and slower once larger batches stream long
+  // splits (batch 4 / 8 at L = 8192: +0.2 / +1.0 us, at L = 32768: +3 us),
+  // so the launcher picks by tiles per wave and pair count.
+  h8 qop[LINE ? 2 : 4];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
+  for (int t = 0; t < (LINE ? 2 : 4); ++t) {
+    const int head = LINE ? (n16 & 7) : n16;
+    const int chunk = LINE ? 8 * t + 2 * g4 + (n16 >> 3) : g4 + 4 * t;
     u4 raw = {0, 0, 0, 0};
-    if (n16 < G) raw = ld16(a.q + q_base + (size_t)n16 * kD + (g4 + 4 * t) * 8);
+    if (head < G) raw = ld16(a.q + q_base + (size_t)head * kD + chunk * 8);
     qop[t] = __builtin_bit_cast(h8, raw);
   }
+  // Tile key held in slot j (j = 0..3) of lane group g4 after the scores:
+  // 4 g4 + j for the plain layout; key_of(j) = 2 g4 + (j & 1) + 8 (j >> 1)
+  // after the LINE fold.  That is also the key order of the P^T operand
+  // below, so LDS row 4 g4 + j of the V tile must hold that key.  V is
+  // always loaded four whole consecutive rows (1 KB) per instruction --
+  // vt[j] of lane group g4 is key 4 g4 + j -- and for LINE the permutation
+  // is applied to the LDS row it is written to: key k goes to row
+  // v_row(k) = 4 ((k & 7) >> 1) + (k & 1) + 2 (k >> 3).
+  auto key_of = [&](int j) { return LINE ? 2 * g4 + (j & 1) + 8 * (j >> 1) : 4 * g4 + j; };
+  auto v_row = [](int k) { return LINE ? 4 * ((k & 7) >> 1) + (k & 1) + 2 * (k >> 3) : k; };
+  // LINE: lanes n16 >= 8 fold entries that are not scores; their scale is
+  // zero, which keeps them finite and equal to zero (a multiply, not a
+  // select, so the DPP before it always runs with every lane enabled).
+  const float lane_scale = (!LINE || n16 < 8) ? a.scale_log2 : 0.0f;
 
   const int t_begin = split * a.tps;
   const int t_end = min(a.ntiles, t_begin + a.tps);
@@ -156,12 +199,24 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
   float m_run = kNegInf;  // per head n16 (uniform over g4)
   float l_run = 0.0f;     // partial over this lane's keys
 
+  // LINE: kt[2 kg + t] = key group kg, line t; plain: kt[t] = chunks
+  // g4 + 4t of key n16.  vt[j]: V row 4 g4 + j of the tile.
   auto load_tile = [&](u4 (&kt)[4], u4 (&vt)[4], int tile) {
     const int row0 = tile * kTile;
-    const int kr = min(row0 + n16, last_row);
+    if constexpr (LINE) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-      kt[t] = ld_stream(Kp + (size_t)kr * kD + (g4 + 4 * t) * 8);
+      for (int kg = 0; kg < 2; ++kg) {
+        const int kr = min(row0 + 8 * kg + (n16 >> 1), last_row);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          kt[2 * kg + t] =
+              ld_stream(Kp + (size_t)kr * kD + (8 * t + 2 * g4 + (n16 & 1)) * 8);
+      }
+    } else {
+      const int kr = min(row0 + n16, last_row);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) kt[t] = ld_stream(Kp + (size_t)kr * kD + (g4 + 4 * t) * 8);
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int vr = min(row0 + 4 * g4 + j, last_row);
@@ -169,34 +224,56 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
     }
   };
 
-  // V^T operands come from a per-wave row-major copy of the V tile in LDS,
-  // read back with ds_read_b64_tr_b16: lane 16g + 4r + q supplies the
-  // address of V[4g + r][d0 + 4q] and receives V[4g .. 4g+3][d0 + (lane & 15)],
-  // the A-operand layout of v_mfma_f32_16x16x16_f16 for O^T = V^T P^T.
+  // V^T operands come from a per-wave row-major copy of the V tile in LDS
+  // (rows in the key order above), read back with ds_read_b64_tr_b16: lane
+  // 16g + 4r + q supplies the address of LDS row 4g + r, column d0 + 4q, and
+  // receives rows 4g .. 4g+3 of column d0 + (lane & 15) -- tile keys
+  // key_of(0..3) of lane group g -- the A-operand layout of
+  // v_mfma_f32_16x16x16_f16 for O^T = V^T P^T.
   _Float16* vbuf = &s_v[wave][0][0];
   auto compute_tile = [&](const u4 (&kt)[4], const u4 (&vt)[4], int tile) {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      *reinterpret_cast<u4*>(vbuf + (4 * g4 + j) * kVStride + 8 * n16) = vt[j];
+      *reinterpret_cast<u4*>(vbuf + v_row(4 * g4 + j) * kVStride + 8 * n16) = vt[j];
 
-    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-          __builtin_bit_cast(h8, kt[t]), qop[t], acc, 0, 0, 0);
-
-    const int key0 = tile * kTile + 4 * g4;
+    // s[j]: scaled score of tile key key_of(j) (-inf past L).
     float s[4];
+    if constexpr (LINE) {
+      f4 d[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      s[i] = (key0 + i < a.L) ? acc[i] * a.scale_log2 : kNegInf;
+      for (int kg = 0; kg < 2; ++kg) {
+        d[kg] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          d[kg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              __builtin_bit_cast(h8, kt[2 * kg + t]), qop[t], d[kg], 0, 0, 0);
+      }
+      // key_of(j) = 8 kg + 2 g4 + r with kg = j >> 1, r = j & 1
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f4& dk = d[j >> 1];
+        const int r = j & 1;
+        s[j] = (dk[2 * r] + dpp<kRowRor8>(dk[2 * r + 1])) * lane_scale;
+      }
+    } else {
+      f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, kt[t]), qop[t],
+                                                     acc, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s[j] = acc[j] * lane_scale;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (tile * kTile + key_of(j) >= a.L) s[j] = kNegInf;
     float tmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
     tmax = fmaxf(tmax, xor_lanes(tmax, 16));
     tmax = fmaxf(tmax, xor_lanes(tmax, 32));
     const float m_new = fmaxf(m_run, tmax);
     const float alpha = fast_exp2(m_run - m_new);
-    // P^T operand: lane (g4, n16) holds P[keys 4g4..4g4+3][head n16], the
-    // accumulator layout of the score MFMA.  p is rounded to fp16 for the
+    // P^T operand: lane (g4, n16) holds P[key key_of(j)][head n16] in slot
+    // j, the order the V tile was written in.  p is rounded to fp16 for the
     // product (as the reference stage rounds p before P.V) and the exp-sum
     // adds the rounded values, so numerator and denominator agree.
     h4 pb;
@@ -260,6 +337,10 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
   }
   __syncthreads();
 
+  // With S > 1 a split's partial record is its running max m_s and exp-sum
+  // l_s (base 2) and its unnormalised output o_s, all fp32.  (fp16 records
+  // of o_s / l_s, half the bytes, measured 0.45 us slower per call at
+  // batch 1, L = 8192 and 32768.)
   for (int idx = threadIdx.x; idx < G * kD; idx += kThreads) {
     const int h = idx / kD, d = idx % kD;
     float M = kNegInf;
@@ -458,21 +539,26 @@ __global__ __launch_bounds__(256) void f4_combine(F4Args a, int G) {
 
 using F4Fn = void (*)(F4Args);
 
-F4Fn pick_kernel(int G, int waves) {
+template <bool LINE>
+F4Fn pick_kernel_layout(int G, int waves) {
   if (waves == 8) {
     switch (G) {
-      case 1: return f4_kernel<1, 8>;
-      case 2: return f4_kernel<2, 8>;
-      case 4: return f4_kernel<4, 8>;
-      default: return f4_kernel<8, 8>;
+      case 1: return f4_kernel<1, 8, LINE>;
+      case 2: return f4_kernel<2, 8, LINE>;
+      case 4: return f4_kernel<4, 8, LINE>;
+      default: return f4_kernel<8, 8, LINE>;
     }
   }
   switch (G) {
-    case 1: return f4_kernel<1, 4>;
-    case 2: return f4_kernel<2, 4>;
-    case 4: return f4_kernel<4, 4>;
-    default: return f4_kernel<8, 4>;
+    case 1: return f4_kernel<1, 4, LINE>;
+    case 2: return f4_kernel<2, 4, LINE>;
+    case 4: return f4_kernel<4, 4, LINE>;
+    default: return f4_kernel<8, 4, LINE>;
   }
+}
+
+F4Fn pick_kernel(int G, int waves, bool line) {
+  return line ? pick_kernel_layout<true>(G, waves) : pick_kernel_layout<false>(G, waves);
 }
 
 size_t round256(size_t n) { return (n + 255) / 256 * 256; }
@@ -485,8 +571,8 @@ int f4_max_splits(int G) {
   return 256;
 }
 
-// Workspace: [tickets: pairs x u32][ml: pairs x G x S float2][opart], each
-// region 256-byte aligned.
+// Workspace: [tickets: pairs x u32][ml: pairs x G x S float2][opart: pairs x
+// S x G x D fp32], the first two regions 256-byte aligned.
 size_t f4_workspace_bytes(int B, int Hq, int Hkv, int S, int D) {
   const int G = Hq / Hkv;
   const size_t pairs = (size_t)B * Hkv;
@@ -508,7 +594,7 @@ int f4_choose_splits(int B, int Hkv, int L, int cu_count) {
 
 hipError_t launch_f4(const void* q, const void* k, const void* v, void* o,
                      void* ws, int B, int Hq, int Hkv, int L, int D, int S,
-                     float scale, hipStream_t stream) {
+                     float scale, hipStream_t stream, bool allow_fused_merge) {
   const int G = Hq / Hkv;
   const int pairs = B * Hkv;
   F4Args a;
@@ -533,14 +619,20 @@ hipError_t launch_f4(const void* q, const void* k, const void* v, void* o,
   a.ticket = reinterpret_cast<unsigned*>(base);
   a.ml = base ? reinterpret_cast<float2*>(base + ticket_bytes) : nullptr;
   a.opart = base ? reinterpret_cast<float*>(base + ticket_bytes + ml_bytes) : nullptr;
-  a.fused_merge = tuning().f4_merge;
+  a.fused_merge = allow_fused_merge ? tuning().f4_merge : 0;
   a.xcd_map = (pairs % 8 == 0) ? 1 : 0;
   a.scale_log2 = scale * kLog2e;
   (void)D;
   // 8 waves once a split has a tile for each (measured: 10% faster than 4
   // at batch 4, L = 1024, where a split holds 8 tiles); 4 below that.
   int waves = tuning().f4_waves > 0 ? tuning().f4_waves : (a.tps >= 8 ? 8 : 4);
-  hipLaunchKernelGGL(pick_kernel(G, waves), dim3(pairs * a.S), dim3(waves * kWave), 0,
+  // Whole-line K loads when a wave walks at most 2 tiles or there are at
+  // most 8 (batch, kv-head) pairs; the plain layout streams long splits of
+  // larger batches faster (see f4_kernel).
+  const int tiles_per_wave = (a.tps + waves - 1) / waves;
+  const bool line = tuning().f4_line == 1 ||
+                    (tuning().f4_line == 0 && (tiles_per_wave <= 2 || pairs <= 8));
+  hipLaunchKernelGGL(pick_kernel(G, waves, line), dim3(pairs * a.S), dim3(waves * kWave), 0,
                      stream, a);
   if (a.S > 1 && !a.fused_merge) {
     const hipError_t e = hipGetLastError();

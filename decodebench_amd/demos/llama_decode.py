@@ -97,42 +97,96 @@ def f2_sequence() -> Sequence:
     return seq
 
 
-def f4_sequence(scale: float = 1.0) -> Sequence:
+def _qk(q, K):
+    """fp16 q.K^T per KV head: [B,Hkv,L,G] (the right operand, q, is the
+    small contiguous one)."""
+    import torch
+
+    B, Hq, D = q.shape
+    Hkv = K.shape[1]
+    qt = q.reshape(B, Hkv, Hq // Hkv, D).transpose(-1, -2).contiguous()
+    return torch.matmul(K, qt)
+
+
+def _scores_f32(qk, scale: float):
+    """[B,Hkv,L,G] fp16 -> scaled fp32 scores [B,Hq,L], contiguous, made by
+    one conversion kernel (plus an in-place scale)."""
+    import torch
+
+    B, Hkv, L, G = qk.shape
+    if G == 1:
+        out = qk.reshape(B, Hkv, L).float()
+    else:
+        out = qk.transpose(-1, -2).to(torch.float32, memory_format=torch.contiguous_format)
+    if scale != 1.0:
+        out.mul_(scale)
+    return out.view(B, Hkv * G, L)
+
+
+def _weighted_v(p16, V):
+    import torch
+
+    B, Hq, L = p16.shape
+    Hkv = V.shape[1]
+    return torch.matmul(p16.view(B, Hkv, Hq // Hkv, L), V).view(B, Hq, V.shape[3])
+
+
+def f4_sequence(scale: float = 1.0, split_stages: bool = False) -> Sequence:
     """scores -> softmax -> weighted_v with grouped query heads.
 
-    q [B,Hq,D], K/V [B,Hkv,L,D]; query head h reads KV head h // (Hq/Hkv)."""
+    q [B,Hq,D], K/V [B,Hkv,L,D]; query head h reads KV head h // (Hq/Hkv).
+    With ``split_stages`` every intermediate is a declared stage output, so
+    the byte model sees all of them and no stage allocates a temporary:
+    qk (fp16 q.K^T) -> scores (fp32, scaled) -> softmax -> probs16 (the fp16
+    probabilities P.V reads) -> weighted_v.  Without it the three stages
+    keep the reference demo's shape (llama_decode.py:120-134)."""
     import torch
 
     seq = Sequence("f4")
 
-    @seq.stage
-    def scores(q, K):
-        B, Hq, D = q.shape
-        Hkv = K.shape[1]
-        qt = q.reshape(B, Hkv, Hq // Hkv, D).transpose(-1, -2).contiguous()
-        s = torch.matmul(K, qt)                        # fp16 [B,Hkv,L,G]
-        return s.transpose(-1, -2).float().mul(scale).reshape(B, Hq, K.shape[2])
+    if split_stages:
+        @seq.stage
+        def qk(q, K):
+            return _qk(q, K)
+
+        @seq.stage
+        def scores(qk):
+            return _scores_f32(qk, scale)
+    else:
+        @seq.stage
+        def scores(q, K):
+            return _scores_f32(_qk(q, K), scale)
 
     @seq.stage
-    def softmax(s):
-        return torch.softmax(s, dim=-1)
+    def softmax(scores):
+        return torch.softmax(scores, dim=-1)
 
-    @seq.stage
-    def weighted_v(p, V):
-        B, Hq, L = p.shape
-        Hkv = V.shape[1]
-        pg = p.half().reshape(B, Hkv, Hq // Hkv, L)
-        return torch.matmul(pg, V).reshape(B, Hq, V.shape[3])
+    if split_stages:
+        @seq.stage
+        def probs16(softmax):
+            return softmax.half()
+
+        @seq.stage
+        def weighted_v(probs16, V):
+            return _weighted_v(probs16, V)
+    else:
+        @seq.stage
+        def weighted_v(softmax, V):
+            return _weighted_v(softmax.half(), V)
 
     return seq
 
 
 def _linear_fp8(a, W, s):
-    """The fp8 projection stage: e4m3 weights dequantised exactly, fp32
-    accumulation, the row scale applied before the fp16 rounding."""
-    import torch
+    """The unfused e4m3 projection stage: the library's plain GEMV
+    (``db_gemv``, one launch) on e4m3 weights with per-row scales, fp32
+    accumulation, the row scale applied before the fp16 rounding -- the
+    counterpart of the reference's unfused gemv kernel
+    (validation/src/kernels/unfused/gemv.cu:15-48).  Its bytes are the
+    weights and scales it reads: nothing is dequantised into memory."""
+    from decodebench_amd import ops
 
-    return (torch.nn.functional.linear(a.float(), W.float()) * s).half()
+    return ops.gemv(a, W, w_scale=s)
 
 
 def f1_fp8_sequence(eps: float = 1e-6) -> Sequence:
@@ -174,9 +228,11 @@ def f2_fp8_sequence() -> Sequence:
 
 def layer_sequence(n_q_heads: int, scale: float, eps: float = 1e-6,
                    fp8: bool = False) -> Sequence:
-    """The decode-layer chain as single-op torch stages: rmsnorm, QKV, the
-    query heads of QKV (copied: a stage returns a tensor of its own), scores,
-    softmax, weighted V, O projection, rmsnorm, gate, up, SwiGLU, down.
+    """The decode-layer chain as single-op stages: rmsnorm, QKV, the query
+    heads of QKV (copied: a stage returns a tensor of its own), q.K^T, fp32
+    scores, softmax, fp16 probabilities, weighted V, O projection, rmsnorm,
+    gate, up, SwiGLU, down.  Torch ops, except that the e4m3 projections run
+    on the library's plain GEMV (see :func:`_linear_fp8`).
 
     The new token's k and v columns of QKV are not appended to the cache:
     the chain measures the decode read path over a given KV cache."""
@@ -208,23 +264,25 @@ def layer_sequence(n_q_heads: int, scale: float, eps: float = 1e-6,
         return qkv[:, : n_q_heads * _HEAD_DIM].reshape(B, n_q_heads, _HEAD_DIM).clone()
 
     @seq.stage
-    def scores(q_heads, K):
-        B, Hq, D = q_heads.shape
-        Hkv = K.shape[1]
-        qt = q_heads.reshape(B, Hkv, Hq // Hkv, D).transpose(-1, -2).contiguous()
-        s = torch.matmul(K, qt)
-        return s.transpose(-1, -2).float().mul(scale).reshape(B, Hq, K.shape[2])
+    def qk(q_heads, K):
+        return _qk(q_heads, K)
+
+    @seq.stage
+    def scores(qk):
+        return _scores_f32(qk, scale)
 
     @seq.stage
     def softmax(scores):
         return torch.softmax(scores, dim=-1)
 
     @seq.stage
-    def weighted_v(softmax, V):
-        B, Hq, L = softmax.shape
-        Hkv = V.shape[1]
-        pg = softmax.half().reshape(B, Hkv, Hq // Hkv, L)
-        return torch.matmul(pg, V).reshape(B, Hq * V.shape[3])
+    def probs16(softmax):
+        return softmax.half()
+
+    @seq.stage
+    def weighted_v(probs16, V):
+        B = probs16.shape[0]
+        return _weighted_v(probs16, V).view(B, -1)
 
     if fp8:
         @seq.stage
@@ -492,7 +550,7 @@ def build_config(name: str, batch: int = 1, L: int = 8192, n_splits: int | None 
         Vc = _randn(gen, (B, Hkv, L, D), device=device)
         inputs = {"q": q, "K": Kc, "V": Vc}
         scale = 1.0 / math.sqrt(D)
-        seq = f4_sequence(scale)
+        seq = f4_sequence(scale, split_stages=True)
         fused = lambda inp: ops.f4_flashdecode(inp["q"], inp["K"], inp["V"], scale=scale,  # noqa: E731
                                                n_splits=n_splits)
         big = ("K", "V")

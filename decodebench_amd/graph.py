@@ -1,26 +1,50 @@
-"""Graph capture and replay with an explicit success/failure result.
+"""Record a body of GPU work once as a hipGraph, then replay it.
 
-On ROCm ``torch.cuda.CUDAGraph`` records a hipGraph; replay launches the whole
-recorded chain with one submission, which is what ``delta_launch`` measures
-against plain stream launches.
+On ROCm ``torch.cuda.CUDAGraph`` is a hipGraph: a replay submits the whole
+recorded chain at once, which is what ``Sequence.profile`` sets against
+stream launches of the same stages (Δ_launch).
 
-Behaviour follows ``src/decodebench/graph.py:9-88`` of the reference: the body
-is warmed up on a side stream, captured into a graph (optionally in a shared
-memory pool), and a capture failure is returned as ``Captured(ok=False)``
-rather than raised.  After a failed capture torch can leave its device RNG
-generator registered with the aborted graph; a trivial capture that succeeds
-clears that state, and any error in that clean-up is reported in ``reason``.
+Interface kept from the reference (src/decodebench/graph.py:9-21):
+``try_capture(body, warmup_iters=3, pool=None)`` returns a ``Captured`` and
+never raises for a body that cannot be captured; ``Captured.ok`` says
+whether it could, ``reason`` why not, and ``replay()`` of a failed capture
+raises ``RuntimeError("cannot replay: capture failed (...)")``.
+
+How it records:
+
+* Every device has one recording stream, made on first use and kept.  The
+  warm-up calls and the capture both run on it, so the blocks the caching
+  allocator hands out while warming up already belong to the stream the
+  graph records on, and the caller's stream is never put in capture mode.
+  The recording stream waits for the caller's stream before the warm-up
+  (pending writes of the inputs), and the caller's stream waits for it
+  afterwards.
+* The capture is opened and closed explicitly, so a body that raises while
+  recording still has its capture closed, and the body's error and the
+  closing error are reported together.
+* A capture that fails after it began leaves torch's device random
+  generators marked as capturing (their capture epilogue never ran), after
+  which ``torch.randn`` on that device raises.  ``_reset_generators``
+  records an empty graph on the recording stream: its opening and closing
+  run the generators' prologue and epilogue and leave them idle.  If that
+  fails as well, its error is appended to ``reason``.
 """
 
 from __future__ import annotations
 
+import threading
 import warnings
 from dataclasses import dataclass
-from typing import Callable
+from typing import Callable, Optional
+
+_recording_streams: dict = {}
+_recording_lock = threading.Lock()
 
 
 @dataclass
 class Captured:
+    """Outcome of :func:`try_capture`: a replayable graph, or why there is none."""
+
     ok: bool
     reason: str = ""
     _graph: object = None
@@ -31,56 +55,89 @@ class Captured:
         self._graph.replay()
 
 
-def try_capture(body: Callable[[], None], warmup_iters: int = 3,
-                pool=None) -> Captured:
-    """Warm ``body`` up on a side stream, then capture it into a graph.
+def try_capture(body: Callable[[], None], warmup_iters: int = 3, pool=None) -> Captured:
+    """Run ``body`` ``warmup_iters`` times, then record one call of it.
 
-    ``pool`` is an optional ``torch.cuda.graph_pool_handle()`` shared by graphs
-    that always replay one after another in capture order.
-    """
+    ``pool`` is an optional ``torch.cuda.graph_pool_handle()`` for graphs that
+    always replay one after another in capture order and may share memory.
+    Errors of the warm-up calls propagate: they are errors of the body, not
+    of capturing it."""
     import torch
 
-    warm = torch.cuda.Stream()
-    warm.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(warm):
+    caller = torch.cuda.current_stream()
+    rec = _recording_stream(caller.device)
+    rec.wait_stream(caller)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(rec):
         for _ in range(warmup_iters):
             body()
-    torch.cuda.current_stream().wait_stream(warm)
-
-    graph = torch.cuda.CUDAGraph()
-    try:
-        with torch.cuda.graph(graph, pool=pool):
-            body()
-    except Exception as exc:  # capture failures come in many types
-        reason = f"{type(exc).__name__}: {exc}"
-        problem = _clear_generator_registration()
-        if problem:
-            reason += (f" [additionally, RNG-registration cleanup failed: "
-                       f"{problem}; torch.randn on this device may raise until "
-                       "the process restarts]")
-        return Captured(ok=False, reason=reason)
-    return Captured(ok=True, _graph=graph)
+        rec.synchronize()
+        failure = _record(graph, body, pool)
+    caller.wait_stream(rec)
+    if failure is None:
+        return Captured(ok=True, _graph=graph)
+    del graph
+    leftover = _reset_generators(rec)
+    if leftover:
+        failure += (f"; resetting the device random generators afterwards failed too "
+                    f"({leftover}), so random ops on this device may raise until the "
+                    f"process restarts")
+    return Captured(ok=False, reason=failure)
 
 
-def _clear_generator_registration() -> str:
-    """Run one trivial, successful capture; return "" or the error text."""
+def _recording_stream(device):
     import torch
 
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    with _recording_lock:
+        stream = _recording_streams.get(key)
+        if stream is None:
+            stream = torch.cuda.Stream(device=key)
+            _recording_streams[key] = stream
+    return stream
+
+
+def _describe(exc: BaseException) -> str:
+    return f"{type(exc).__name__}: {exc}"
+
+
+def _record(graph, body: Callable[[], None], pool) -> Optional[str]:
+    """Capture one call of ``body`` into ``graph`` on the current stream.
+
+    Returns None on success, else the error text.  Once the capture has been
+    opened it is always closed, whatever the body does."""
     try:
-        if torch.cuda.is_current_stream_capturing():
-            return "current stream is still in capture mode; skipped cleanup"
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        scratch = torch.zeros(1, device="cuda")   # allocated before capture
-        g = torch.cuda.CUDAGraph()
-        with warnings.catch_warnings():
+        graph.capture_begin(pool=pool)
+    except Exception as exc:  # the capture never started
+        return _describe(exc)
+    body_error = None
+    try:
+        body()
+    except Exception as exc:  # anything the body raises ends the recording
+        body_error = exc
+    try:
+        graph.capture_end()
+    except Exception as exc:
+        if body_error is None:
+            return _describe(exc)
+        return f"{_describe(body_error)} (closing the capture: {_describe(exc)})"
+    return None if body_error is None else _describe(body_error)
+
+
+def _reset_generators(stream) -> str:
+    """Record an empty graph on ``stream`` so that torch runs the capture
+    epilogue of its device generators; "" on success, else the error."""
+    import torch
+
+    empty = torch.cuda.CUDAGraph()
+    try:
+        with torch.cuda.stream(stream), warnings.catch_warnings():
+            # torch warns that a graph without nodes was captured; that is the point
             warnings.simplefilter("ignore")
-            with torch.cuda.stream(side):
-                g.capture_begin()
-                scratch.fill_(0.0)
-                g.capture_end()
-        torch.cuda.current_stream().wait_stream(side)
-        del g, scratch
-        return ""
-    except Exception as exc:  # never mask the original capture failure
-        return f"{type(exc).__name__}: {exc}"
+            empty.capture_begin()
+            empty.capture_end()
+    except Exception as exc:
+        return _describe(exc)
+    finally:
+        del empty
+    return ""

@@ -35,6 +35,8 @@ _lock = threading.Lock()
 _lib = None
 _cu_cache: dict[int, int] = {}
 _ws_cache: dict[tuple, object] = {}
+_captured_ws: dict[tuple, object] = {}  # workspaces made under graph capture (kept alive)
+_tuned: dict[str, int] = {}      # db_tune values set through tune()
 
 _p = C.c_void_p
 _i = C.c_int
@@ -68,6 +70,8 @@ def load_library():
             "db_f4_workspace_bytes": (C.c_size_t, [_i, _i, _i, _i, _i, _i]),
             "db_f4_splitkv": (_i, [_p, _p, _p, _p, _p, C.c_size_t, _i, _i, _i, _i, _i, _i,
                                    C.c_float, _p]),
+            "db_stream_read": (_i, [_p, C.c_size_t, _i, C.c_uint, _p, _p]),
+            "db_stream_capture_id": (_i, [_p, C.POINTER(C.c_ulonglong)]),
             "db_tune": (_i, [C.c_char_p, _i]),
             "db_null_kernel": (_i, [_p]),
         }
@@ -151,9 +155,30 @@ def null_kernel(device=None) -> None:
     _check(rc, "db_null_kernel")
 
 
+def stream_read(src, kb_per_wave: int = 8, sink=None) -> None:
+    """Launch the read-only streaming probe over all of ``src`` (a contiguous
+    GPU tensor of a whole number of ``kb_per_wave`` KB) on the current stream.
+
+    ``src`` should hold zeros: the probe stores to ``sink`` only when the
+    folded data equals its (non-zero) magic value, so it then writes
+    nothing.  ``sink`` (int32, >= nbytes/16 elements) is allocated when not
+    given; pass one to keep the call allocation-free (graph capture)."""
+    import torch
+
+    _require(src, "src")
+    nbytes = src.numel() * src.element_size()
+    if sink is None:
+        sink = torch.empty(max(1, nbytes // 16), dtype=torch.int32, device=src.device)
+    with _on_device(src):
+        rc = load_library().db_stream_read(src.data_ptr(), nbytes, int(kb_per_wave), 0x9E3779B9,
+                                           sink.data_ptr(), _stream_ptr(src))
+    _check(rc, "db_stream_read")
+
+
 def tune(key: str, value: int) -> None:
     """Set a launch-geometry knob of the library (for tuning sweeps)."""
     _check(load_library().db_tune(key.encode(), int(value)), "db_tune")
+    _tuned[key] = int(value)
 
 
 def _weights(W, w_scale, name: str, N: int, K: int):
@@ -296,15 +321,26 @@ def f4_default_splits(B: int, Hkv: int, L: int, device=None) -> int:
 
 
 def f4_workspace(B: int, Hq: int, Hkv: int, L: int, D: int, S: int, device):
-    """Workspace for db_f4_splitkv, cached per size, device and current stream.
+    """Workspace for db_f4_splitkv (None when S = 1).
 
-    It is zero-filled once, when allocated; every call leaves its split
-    tickets at zero again, so one buffer serves every later call of that size
-    on that stream, whose calls run in order, also under graph capture.
-    Calls on different streams get different buffers, so they may overlap.
-    (Replays of two graphs captured on one stream share its buffer and must
-    not overlap.)  torch draws streams from a fixed pool per device, so the
-    cache stays bounded."""
+    Outside graph capture it is cached per size, device and current stream
+    and zero-filled once, when allocated: every call leaves its split
+    tickets at zero again, so one buffer serves every later call of that
+    size on that stream, whose calls run in order.  Calls on different
+    streams get different buffers, so they may overlap.  torch draws streams
+    from a fixed pool per device, so the cache stays bounded.
+
+    Under graph capture each capture (each hipGraph being recorded) gets a
+    workspace of its own from the graph's memory pool, shared by the calls
+    of that size it records (they run in stream order on replay), never the
+    cached one: graphs captured on torch's one capture stream would
+    otherwise share it, and replaying two of them at once on different
+    streams would mix their partial records.  Those workspaces stay
+    referenced until :func:`release_captured_workspaces`, so the pool never
+    hands their memory to another graph while one that uses it can still be
+    replayed.  They are zero-filled only when the in-launch merge
+    (``tune("f4_merge", 1)``), the one reader of the tickets, is on;
+    otherwise nothing is recorded into the graph besides the F4 launches."""
     import torch
 
     nbytes = int(load_library().db_f4_workspace_bytes(B, Hq, Hkv, L, D, S))
@@ -312,12 +348,33 @@ def f4_workspace(B: int, Hq: int, Hkv: int, L: int, D: int, S: int, device):
         return None
     dev = torch.device(device)
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
-    key = (idx, torch.cuda.current_stream(idx).cuda_stream, nbytes)
+    stream = torch.cuda.current_stream(idx).cuda_stream
+    if torch.cuda.is_current_stream_capturing():
+        cid = C.c_ulonglong(0)
+        _check(load_library().db_stream_capture_id(stream, C.byref(cid)),
+               "db_stream_capture_id")
+        key = (idx, stream, cid.value, nbytes, _tuned.get("f4_merge", 0))
+        ws = _captured_ws.get(key)
+        if ws is None:
+            make = torch.zeros if _tuned.get("f4_merge", 0) else torch.empty
+            ws = make(nbytes, dtype=torch.uint8, device=dev)
+            _captured_ws[key] = ws
+        return ws
+    key = (idx, stream, nbytes)
     ws = _ws_cache.get(key)
     if ws is None:
         ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
         _ws_cache[key] = ws
     return ws
+
+
+def release_captured_workspaces() -> int:
+    """Drop the references to the F4 workspaces made under graph capture;
+    call it once every graph that recorded F4 calls has been destroyed.
+    Returns how many were released."""
+    n = len(_captured_ws)
+    _captured_ws.clear()
+    return n
 
 
 def f4_flashdecode(q, K, V, scale: float | None = None, n_splits: int | None = None,
@@ -353,3 +410,4 @@ def f4_flashdecode(q, K, V, scale: float | None = None, n_splits: int | None = N
                                           _stream_ptr(q))
     _check(rc, "db_f4_splitkv")
     return o
+

@@ -108,7 +108,7 @@ int db_gemv(const void* x, const void* W, const float* w_scale, void* y,
 
 /* Split count the library picks for F4 when the caller has no preference:
  * about one (batch, kv-head, split) workgroup per CU of `cu_count` while
- * every split keeps at least four 16-row tiles.  Replaces the fixed L/128 default and
+ * every split keeps at least eight 16-row tiles.  Replaces the fixed L/128 default and
  * DECODEBENCH_F4_SPLITS override of the reference harness
  * (validation/src/bench/bench_variant.cu:714-719). */
 int db_f4_default_splits(int B, int Hkv, int L, int cu_count);
@@ -137,18 +137,30 @@ int db_f4_splitkv(const void* q, const void* k, const void* v, void* o,
                   void* ws, size_t ws_bytes, int B, int Hq, int Hkv, int L,
                   int D, int S, float scale, void* stream);
 
-/* Launch an empty kernel (one workgroup of 256 threads) on `stream`: the
- * launch-overhead probe of the calibration.  Replaces null_kernel and its
- * 500-launch stream / graph timing loop (validation/src/bench/
- * calibrate.cu:42-104), whose timing the Python calibration does with HIP
- * events. */
-int db_null_kernel(void* stream);
+/* Read `bytes` bytes at `src` once and discard them: the single-launch
+ * streaming floor of this GPU, used by the calibration (bytes one launch
+ * moves vs its time) and as a read-only, known-size reference for the HBM
+ * traffic counters.  Every wave reads one contiguous chunk of kb_per_wave KB
+ * (4, 8 or 16) with 16-byte non-temporal loads, 1 KB per wave-wide load
+ * instruction, all issued before any is used.  The loaded words are folded
+ * into one value per lane, stored to sink[] only if it equals `magic`
+ * (choose a value that cannot occur, e.g. with src zero-filled and magic
+ * non-zero), so the kernel reads `bytes` and writes nothing.
+ * Contract: src and sink 16-byte aligned and non-null, bytes a positive
+ * multiple of kb_per_wave * 1024, sink holding bytes / 16 unsigned words.
+ * Replaces the read side of the cuBLAS bandwidth reference of the G2 gate
+ * (validation/src/bench/calibrate.cu:113-230) as the measure of what one
+ * launch can stream; no kernel of the reference is its counterpart. */
+int db_stream_read(const void* src, size_t bytes, int kb_per_wave, unsigned magic,
+                   unsigned* sink, void* stream);
 
 /* Launch-geometry knobs for tuning sweeps: "gemv_waves_per_cu" (<= 0: the
  * default, 32), "gemv_mfma_min_batch" (0: automatic, 3 rows, 2 for the
  * e4m3 gate/up pair), "f4_blocks_per_cu", "f4_min_tiles",
- * "f4_waves" (4 or 8 waves per workgroup, 0: automatic) and "f4_merge" (0: the
- * split merge runs in a second launch, the default; 1: in the same launch).
+ * "f4_waves" (4 or 8 waves per workgroup, 0: automatic), "f4_merge" (0: the
+ * split merge runs in a second launch, the default; 1: in the same launch)
+ * and "f4_line" (F4 score-operand layout: 0 automatic, 1 whole-line K loads,
+ * 2 16 keys x 64 bytes per load).
  * Process-wide; no counterpart in the reference. */
 int db_tune(const char* key, int value);
 

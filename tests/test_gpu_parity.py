@@ -65,6 +65,9 @@ F1_CASES = [
     (1, 4096, 4096, 1 / 64), (1, 4096, 6144, 0.02), (4, 4096, 6144, 0.02),
     (8, 4096, 6144, 0.02), (5, 4096, 512, 0.02), (16, 4096, 1024, 0.02),
     (1, 14336, 4096, 0.01),
+    # config 3 (fused QKV, W [6144, 4096]) at the batch sizes of its sweep that take the MFMA
+    # kernel's 16-row and 32-row passes
+    (16, 4096, 6144, 0.02), (32, 4096, 6144, 0.02),
     # one batch row: 2 rows per wave where (N + 15) / 16 fills every CU with whole 8-wave
     # workgroups (K = 2048, and N = 4095 with a half-empty last group), else 1
     (1, 2048, 8192, 0.02), (1, 4096, 4095, 1 / 64),
@@ -99,7 +102,10 @@ def test_f1_one_dimensional_input_and_determinism():
 
 # ------------------------------------------------------------------- F2
 F2_CASES = [(1, 256, 96), (2, 1024, 300), (1, 4096, 14336), (4, 4096, 14336),
-            (16, 4096, 2048), (3, 4096, 1000)]
+            (16, 4096, 2048), (3, 4096, 1000),
+            # config 2 at B = 16: two batch tiles and alternating register sets on the
+            # MFMA kernel at the full gate/up shape
+            (16, 4096, 14336)]
 
 
 @pytest.mark.parametrize("B,K,N", F2_CASES)
@@ -392,6 +398,32 @@ def test_f4_splitkv_parity(B, Hq, Hkv, L, S):
     assert_parity(o, ref, exact, F4_REL_L2, f"f4 B={B} Hq={Hq} Hkv={Hkv} L={L} S={S}")
 
 
+# Shapes run with each score-operand layout forced (db_tune "f4_line": 1 = whole-line K
+# loads, 2 = 16 keys x 64 bytes); the launcher otherwise picks by tiles per wave.
+F4_LAYOUT_CASES = [(1, 32, 8, 1024, None), (1, 32, 8, 8192, None), (4, 32, 8, 4096, 4),
+                   (1, 64, 8, 100, None), (1, 8, 8, 300, 3), (1, 32, 8, 17, 2),
+                   (2, 16, 8, 257, 5), (1, 16, 16, 2000, 8), (1, 32, 8, 720, 1)]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,L,S", F4_LAYOUT_CASES)
+def test_f4_score_layouts(B, Hq, Hkv, L, S):
+    print(f"[f4-layout] B={B} Hq={Hq} Hkv={Hkv} L={L} S={S}", flush=True)
+    q, K, V = f4_inputs(B, Hq, Hkv, L, 3500 + B * 7 + L + (S or 0))
+    exact = cref.attention(q.numpy(), K.numpy(), V.numpy())
+    ref = stages.f4(q, K, V)
+    outs = []
+    try:
+        for layout in (1, 2):
+            ops.tune("f4_line", layout)
+            o = ops.f4_flashdecode(q.cuda(), K.cuda(), V.cuda(), n_splits=S)
+            torch.cuda.synchronize()
+            assert_parity(o, ref, exact, F4_REL_L2, f"f4 layout {layout} B={B} L={L} S={S}")
+            outs.append(o.float().cpu().numpy())
+    finally:
+        ops.tune("f4_line", 0)
+    assert rel_l2(outs[0], outs[1]) < 2e-3
+
+
 @pytest.mark.parametrize("L", [8192, 32768])
 def test_f4_full_batch_split_invariance(L):
     """B = 8 at full length: every split count gives the same answer, and
@@ -407,6 +439,24 @@ def test_f4_full_batch_split_invariance(L):
     assert rel_l2(outs[-1][:1], exact0) < F4_REL_L2
     exact7 = cref.attention(q[7:].numpy(), K[7:].numpy(), V[7:].numpy())
     assert rel_l2(outs[-1][7:], exact7) < F4_REL_L2
+
+
+def test_f4_config4_batch4_full_length():
+    """Config 4 at B = 4, L = 32768: batch rows 0 and 3 against the exact
+    oracle (relative L2, which zeros would fail: |o| is about 0.009 here)
+    and the same answer for every split count."""
+    print("[f4-cfg4] B=4 L=32768", flush=True)
+    q, K, V = f4_inputs(4, 32, 8, 32768, 4321)
+    qd, Kd, Vd = q.cuda(), K.cuda(), V.cuda()
+    outs = {s: ops.f4_flashdecode(qd, Kd, Vd, n_splits=s).float().cpu().numpy()
+            for s in (None, 1, 4, 16, 64)}
+    for s, o in outs.items():
+        assert rel_l2(o, outs[None]) < 2e-3, f"S={s}"
+    for row in (0, 3):
+        exact = cref.attention(q[row:row + 1].numpy(), K[row:row + 1].numpy(),
+                               V[row:row + 1].numpy())
+        assert rel_l2(outs[None][row:row + 1], exact) < F4_REL_L2, f"row {row}"
+        assert rel_l2(np.zeros_like(exact), exact) > 0.5   # the bound rejects zeros
 
 
 def test_f4_workspace_reuse_is_deterministic():
@@ -457,6 +507,47 @@ def test_f4_concurrent_streams_get_their_own_workspace():
     for i in range(2):
         for o in outs[i]:
             assert torch.equal(o, ref[i])
+
+
+@pytest.mark.parametrize("merge", [0, 1])
+def test_f4_graphs_replayed_concurrently_use_their_own_workspaces(merge):
+    """Two graphs captured on torch's capture stream, each holding F4 calls
+    of the same shape, replayed at the same time on two streams: each
+    capture has its own workspace, so both graphs give their eager
+    results on every replay (with the split merge in a second launch, and
+    with the in-launch merge, whose tickets must start at zero)."""
+    inputs = [tuple(t.cuda() for t in f4_inputs(1, 32, 8, 8192, 41 + i)) for i in range(2)]
+    try:
+        ops.tune("f4_merge", merge)
+        want = [ops.f4_flashdecode(*d) for d in inputs]
+        torch.cuda.synchronize()
+        graphs, outs = [], []
+        for d in inputs:
+            ops.f4_flashdecode(*d)          # warm-up outside the capture
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                o = [ops.f4_flashdecode(*d) for _ in range(4)]
+            graphs.append(g)
+            outs.append(o)
+        streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+        for rep in range(6):
+            for s in streams:
+                s.wait_stream(torch.cuda.current_stream())
+            for g, s in zip(graphs, streams):
+                with torch.cuda.stream(s):
+                    g.replay()
+            for s in streams:
+                torch.cuda.current_stream().wait_stream(s)
+            torch.cuda.synchronize()
+            for i in range(2):
+                for o in outs[i]:
+                    assert torch.equal(o, want[i]), f"graph {i}, replay {rep}"
+        del graphs
+        torch.cuda.synchronize()
+        assert ops.release_captured_workspaces() >= 2     # one per capture
+    finally:
+        ops.tune("f4_merge", 0)
 
 
 @pytest.mark.parametrize("B,L", [(1, 1024), (1, 8192), (4, 8192), (8, 300)])
@@ -521,7 +612,9 @@ def c_oracle_layer(inp, Hq, fp8):
 
 
 @pytest.mark.parametrize("dtype,B,L", [("f16", 1, 1024), ("fp8", 1, 1024), ("f16", 2, 520),
-                                       ("fp8", 3, 300)])
+                                       ("fp8", 3, 300),
+                                       # config 5 itself: batch 1, KV length 8192
+                                       ("f16", 1, 8192), ("fp8", 1, 8192)])
 def test_decode_layer_chain_parity(dtype, B, L):
     """Config-5 chain at Llama-3-8B width through the fused HIP kernels
     (F1 -> F4 -> O GEMV -> RMSNorm+F2 -> down GEMV) against the torch stage
