@@ -263,6 +263,29 @@ int db_f4_splitkv(const void* q, const void* k, const void* v, void* o,
                     fn);
 }
 
+int db_f4_splitkv_noalloc(const void* q, const void* k, const void* v, void* o,
+                          int B, int Hq, int Hkv, int L, int D, int S,
+                          float scale, void* stream) {
+  const char* fn = "db_f4_splitkv_noalloc";
+  const int rc = check_f4(fn, q, k, v, o, B, Hq, Hkv, L, D, S, scale);
+  if (rc) return rc;
+  const int s_eff = f4_effective_splits(L, S);
+  void* ws = nullptr;
+  if (s_eff > 1) {
+    const size_t need = dbk::f4_workspace_bytes(B, Hq, Hkv, s_eff, D);
+    if (need > DB_F4_SCRATCH_BYTES)
+      return fail(DB_ERR_INVALID,
+                  "%s: %d splits of B=%d x Hq=%d need %zu bytes of partial records, more "
+                  "than the %zu-byte scratch array; use fewer splits or db_f4_splitkv",
+                  fn, s_eff, B, Hq, need, (size_t)DB_F4_SCRATCH_BYTES);
+    const hipError_t e = dbk::f4_scratch_address(&ws);
+    if (e != hipSuccess) return hip_status(e, fn);
+  }
+  return hip_status(dbk::launch_f4(q, k, v, o, ws, B, Hq, Hkv, L, D, s_eff, scale,
+                                   (hipStream_t)stream, /*allow_fused_merge=*/false),
+                    fn);
+}
+
 int db_stream_read(const void* src, size_t bytes, int kb_per_wave, unsigned magic,
                    unsigned* sink, void* stream) {
   const char* fn = "db_stream_read";

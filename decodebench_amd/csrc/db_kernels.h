@@ -77,6 +77,11 @@ hipError_t launch_f4(const void* q, const void* k, const void* v, void* o,
                      void* ws, int B, int Hq, int Hkv, int L, int D, int S,
                      float scale, hipStream_t stream, bool allow_fused_merge = true);
 
+// Bytes of the per-device scratch array behind db_f4_splitkv_noalloc.
+constexpr size_t kF4ScratchBytes = DB_F4_SCRATCH_BYTES;
+// Device address of that array on the current device (looked up once per
+// device with hipGetSymbolAddress).
+hipError_t f4_scratch_address(void** out);
 
 // Read-only streaming probe (stream_probe.hip): `bytes` (a multiple of
 // kb_per_wave KB, kb_per_wave in {4, 8, 16}) read once, kb_per_wave KB per

@@ -52,6 +52,9 @@
 // The merge follows the reference's two-phase split-KV form
 // (validation/src/kernels/fused/f4.cu:160-319): per-split max m, exp-sum l
 // and unnormalised o, merged as o = sum_s e^{m_s-M} o_s / sum_s e^{m_s-M} l_s.
+#include <atomic>
+#include <mutex>
+
 #include "db_device.h"
 #include "db_kernels.h"
 
@@ -640,6 +643,40 @@ hipError_t launch_f4(const void* q, const void* k, const void* v, void* o,
     hipLaunchKernelGGL(f4_combine, dim3(pairs * G), dim3(256), 0, stream, a, G);
   }
   return hipGetLastError();
+}
+
+// ---- scratch of the allocation-free entry point ---------------------------
+// db_f4_splitkv_noalloc keeps its split partial records (the workspace
+// layout above, tickets unused because it always merges in the second
+// launch) in this file-scope device array.  Every GPU the library runs on
+// holds its own copy until the process ends, and every call on that GPU
+// reuses it.  In host code `scratch` names a host-side shadow, not device
+// memory: the device address comes from hipGetSymbolAddress, looked up once
+// per device with that device current, and only that address is passed to
+// the kernels.
+static __device__ __align__(256) unsigned char scratch[kF4ScratchBytes];
+
+hipError_t f4_scratch_address(void** out) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<void*> addr[kMaxDevices];
+  static std::mutex mu;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  void* p = addr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(mu);
+    p = addr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return e;
+      if (!p) return hipErrorInvalidSymbol;
+      addr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return hipSuccess;
 }
 
 }  // namespace dbk

@@ -70,6 +70,8 @@ def load_library():
             "db_f4_workspace_bytes": (C.c_size_t, [_i, _i, _i, _i, _i, _i]),
             "db_f4_splitkv": (_i, [_p, _p, _p, _p, _p, C.c_size_t, _i, _i, _i, _i, _i, _i,
                                    C.c_float, _p]),
+            "db_f4_splitkv_noalloc": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, C.c_float,
+                                           _p]),
             "db_stream_read": (_i, [_p, C.c_size_t, _i, C.c_uint, _p, _p]),
             "db_stream_capture_id": (_i, [_p, C.POINTER(C.c_ulonglong)]),
             "db_tune": (_i, [C.c_char_p, _i]),
@@ -411,3 +413,42 @@ def f4_flashdecode(q, K, V, scale: float | None = None, n_splits: int | None = N
     _check(rc, "db_f4_splitkv")
     return o
 
+
+def f4_flashdecode_noalloc(q, K, V, scale: float | None = None, n_splits: int | None = None,
+                           out=None):
+    """F4 through ``db_f4_splitkv_noalloc``: the same kernels as
+    :func:`f4_flashdecode`, with the split partials in a library-owned
+    device array (``DB_F4_SCRATCH_BYTES`` per GPU) instead of a workspace,
+    so the library allocates nothing.  Pass ``out`` ([B,Hq,D] fp16,
+    contiguous) to allocate nothing on the Python side either.
+
+    Every call on one GPU shares that array: calls that overlap in time on
+    one GPU (concurrent streams or concurrently replayed graphs) race.  Make
+    the first call on a device outside graph capture (it looks up the
+    array's device address)."""
+    import torch
+
+    for t, n in ((q, "q"), (K, "K"), (V, "V")):
+        _require(t, n, torch.float16)
+    if q.dim() != 3 or K.dim() != 4 or K.shape != V.shape:
+        raise ValueError(f"expected q [B,Hq,D] and K, V [B,Hkv,L,D]; got q {tuple(q.shape)}, "
+                         f"K {tuple(K.shape)}, V {tuple(V.shape)}")
+    B, Hq, D = q.shape
+    Bk, Hkv, L, Dk = K.shape
+    if Bk != B or Dk != D:
+        raise ValueError(f"q {tuple(q.shape)} and K {tuple(K.shape)} disagree on B or D")
+    if out is None:
+        out = torch.empty((B, Hq, D), dtype=torch.float16, device=q.device)
+    else:
+        _require(out, "out", torch.float16)
+        if tuple(out.shape) != (B, Hq, D):
+            raise ValueError(f"out must have shape {(B, Hq, D)} (got {tuple(out.shape)})")
+    _same_device((q, "q"), (K, "K"), (V, "V"), (out, "out"))
+    scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    S = f4_default_splits(B, Hkv, L, q.device) if n_splits is None else int(n_splits)
+    with _on_device(q):
+        rc = load_library().db_f4_splitkv_noalloc(q.data_ptr(), K.data_ptr(), V.data_ptr(),
+                                                  out.data_ptr(), B, Hq, Hkv, L, D, S, scale,
+                                                  _stream_ptr(q))
+    _check(rc, "db_f4_splitkv_noalloc")
+    return out

@@ -137,6 +137,46 @@ int db_f4_splitkv(const void* q, const void* k, const void* v, void* o,
                   void* ws, size_t ws_bytes, int B, int Hq, int Hkv, int L,
                   int D, int S, float scale, void* stream);
 
+/* Size of the per-device scratch array behind db_f4_splitkv_noalloc. */
+#define DB_F4_SCRATCH_BYTES ((size_t)4 << 20)
+
+/* F4 without a workspace argument and without any allocation: the same
+ * computation and kernels as db_f4_splitkv, with the split partial records
+ * kept in a library-owned device array of DB_F4_SCRATCH_BYTES (4 MiB) per
+ * GPU, held from the first call on that GPU until the process ends.  The
+ * split merge always runs in the second launch (db_tune "f4_merge" is
+ * ignored), so nothing in the array has to start at zero.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under hipGraph capture that must not call hipMalloc,
+ * tight serving loops, harnesses that forbid allocation).  It calls no
+ * hipMalloc/hipFree; its first call on a device looks up the array's device
+ * address (hipGetSymbolAddress), so make that first call outside stream
+ * capture.
+ * Every call on one GPU shares that GPU's array: calls that overlap in time
+ * on one GPU (concurrent streams, concurrently replayed graphs) race and
+ * give wrong results; serialise them or use db_f4_splitkv with one workspace
+ * per stream.
+ * Contract as db_f4_splitkv, plus: the S' = min(S, ceil(L / 16)) splits must
+ * fit, db_f4_workspace_bytes(B,Hq,Hkv,L,D,S') <= DB_F4_SCRATCH_BYTES, else
+ * DB_ERR_INVALID (checked before any HIP call).  At the library's default
+ * split count (about one workgroup per CU) that holds up to G = 8. */
+int db_f4_splitkv_noalloc(const void* q, const void* k, const void* v, void* o,
+                          int B, int Hq, int Hkv, int L, int D, int S,
+                          float scale, void* stream);
+
+/* Capture state of `stream`: *capture_id is the id of the hipGraph capture
+ * the stream is recording into (unique per capture), or 0 when it is not
+ * capturing.  Host plumbing with no counterpart in the reference: the
+ * Python ops use it to give every capture its own F4 workspace. */
+int db_stream_capture_id(void* stream, unsigned long long* capture_id);
+
+/* Launch an empty kernel (one workgroup of 256 threads) on `stream`: the
+ * launch-overhead probe of the calibration.  Replaces null_kernel and its
+ * 500-launch stream / graph timing loop (validation/src/bench/
+ * calibrate.cu:42-104), whose timing the Python calibration does with HIP
+ * events. */
+int db_null_kernel(void* stream);
+
 /* Read `bytes` bytes at `src` once and discard them: the single-launch
  * streaming floor of this GPU, used by the calibration (bytes one launch
  * moves vs its time) and as a read-only, known-size reference for the HBM

@@ -38,7 +38,7 @@ def test_header_declares_the_entry_points():
                  "db_f2_gateup_swiglu", "db_f2_rmsnorm_gateup_swiglu", "db_gemv",
                  "db_f4_splitkv",
                  "db_f4_workspace_bytes", "db_f4_default_splits", "db_device_cu_count",
-                 "db_tune"):
+                 "db_f4_splitkv_noalloc", "db_tune"):
         assert want in names
 
 
@@ -129,6 +129,28 @@ def test_f4_contract_errors(lib):
     assert call(ws=None) == -1 and "workspace" in last(lib)
     assert call(ws_bytes=16) == -1 and "required" in last(lib)
     assert f(None, P, P, P, P, 1 << 30, 1, 32, 8, 1024, 128, 4, 0.1, None) == -1
+
+
+def test_f4_noalloc_contract_errors(lib):
+    """The allocation-free F4 entry point checks the same contract, and
+    rejects split counts whose partial records exceed its scratch array,
+    before any HIP call."""
+    f = lib.db_f4_splitkv_noalloc
+
+    def call(B=1, Hq=32, Hkv=8, L=1024, D=128, S=4, q=P):
+        return f(q, P, P, P, B, Hq, Hkv, L, D, S, 0.088, None)
+
+    assert call(q=None) == -1 and "null" in last(lib)
+    assert call(D=64) == -1 and "128" in last(lib)
+    assert call(Hq=48, Hkv=4) == -1 and "G=12" in last(lib)
+    assert call(S=0) == -1 and call(S=257) == -1
+    scratch = 4 << 20
+    # B=8, Hkv=8, G=8, 256 splits: 64 pairs x 256 x 8 heads x 128 x 4 B = 64 MiB of partials
+    assert lib.db_f4_workspace_bytes(8, 64, 8, 1 << 16, 128, 256) > scratch
+    assert call(B=8, Hq=64, Hkv=8, L=1 << 16, S=256) == -1
+    assert "scratch" in last(lib) and str(scratch) in last(lib)
+    # S is capped at the tile count first: 256 splits of 16 keys need one split
+    assert lib.db_f4_workspace_bytes(8, 64, 8, 16, 128, 1) == 0
 
 
 def test_f4_workspace_and_split_policy(lib):
