@@ -72,6 +72,11 @@ def parse_args(argv=None):
                          "every fused workload and the decomposition configs' unfused stage "
                          "chains eagerly, each between two delimiter kernels; write the launch "
                          "manifest to MANIFEST and exit")
+    ap.add_argument("--graph", action="store_true",
+                    help="with --profile-pass: replay each fused workload's calls from one "
+                         "hipGraph (back-to-back launches for the kernel trace)")
+    ap.add_argument("--calls", type=int, default=24,
+                    help="with --profile-pass: calls per workload segment")
     ap.add_argument("--sweep-only", metavar="REGEX",
                     help="per-kernel table restricted to matching workloads; skips the "
                          "decomposition and the CPU baseline")
@@ -268,13 +273,22 @@ def f4_partial_bytes(kw: dict, batch: int = 1) -> int:
     return 0 if S <= 1 else 2 * batch * Hq * S * (D + 2) * 4
 
 
-def profile_pass(manifest_path: str, calls: int = 24, warmup: int = 4) -> int:
-    """Launch sequence for decodebench_amd.rocprof: calibration copies first,
-    then each workload's calls eagerly over cache-defeating replicas, between
-    two launches of the library's empty kernel (the segment delimiters).  The
-    fused calls of every profile workload come first, then the unfused torch
-    stage chains of the decomposition configs.  Two warm-up calls precede
-    each segment, outside its delimiters."""
+def profile_pass(manifest_path: str, calls: int = 24, warmup: int = 4,
+                 graph: bool = False) -> int:
+    """Launch sequence for decodebench_amd.rocprof: calibration kernels first
+    (``copy_calls`` device copies of ``copy_bytes``, which read and write that
+    many bytes, then ``read_calls`` launches of the read-only streaming probe
+    over ``read_bytes``), then each workload's calls over cache-defeating
+    replicas, between two launches of the library's empty kernel (the segment
+    delimiters).  The fused calls of every profile workload come first, then
+    the unfused torch stage chains of the decomposition configs.
+
+    Eager (default): the calls are launched one by one, with two warm-up
+    calls before each segment, outside its delimiters.  ``graph=True``: the
+    fused calls of a workload are captured into one hipGraph, replayed once
+    as warm-up, and then replayed between the delimiters, so the kernel
+    trace shows back-to-back launches with no host gaps (the unfused chains
+    stay eager)."""
     import torch
 
     from decodebench_amd import ops
@@ -290,6 +304,25 @@ def profile_pass(manifest_path: str, calls: int = 24, warmup: int = 4) -> int:
         ops.null_kernel()
         torch.cuda.synchronize()
 
+    def graph_segment(case):
+        reps = case.replicas
+        n = len(reps)
+        for r in reps:                  # first calls (workspaces) outside the capture
+            case.fused(r)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(calls):
+                case.fused(reps[i % n])
+        g.replay()                      # warm-up replay
+        torch.cuda.synchronize()
+        ops.null_kernel()
+        g.replay()
+        ops.null_kernel()
+        torch.cuda.synchronize()
+        del g
+        ops.release_captured_workspaces()
+
     ops.load_library()
     copy_bytes, copy_calls = 512 << 20, 3
     src = torch.empty(copy_bytes, dtype=torch.uint8, device="cuda")
@@ -299,15 +332,25 @@ def profile_pass(manifest_path: str, calls: int = 24, warmup: int = 4) -> int:
         dst.copy_(src)
     torch.cuda.synchronize()
     del src, dst
+    read_bytes, read_calls, read_kb = 512 << 20, 3, 4
+    zeros = torch.zeros(read_bytes, dtype=torch.uint8, device="cuda")
+    sink = torch.empty(read_bytes // 16, dtype=torch.int32, device="cuda")
+    for _ in range(read_calls):
+        ops.stream_read(zeros, read_kb, sink)
+    torch.cuda.synchronize()
+    del zeros, sink
     workloads = []
     for label, kw in PROFILE_WORKLOADS:
         case = build_config(gen_device="cuda", **{"batch": 1, **kw})
         n = len(case.replicas)
-        segment(lambda i: case.fused(case.replicas[i % n]), n)
+        if graph:
+            graph_segment(case)
+        else:
+            segment(lambda i: case.fused(case.replicas[i % n]), n)
         workloads.append({"label": label, "kind": "fused", "calls": calls, "warmup": warmup,
                           "kernels_per_call": kernels_per_call(kw),
                           "algorithmic_bytes": case.algorithmic_bytes})
-        log(f"profile pass: {label} x {calls}")
+        log(f"profile pass: {label} x {calls}" + (" (graph)" if graph else ""))
         del case
         torch.cuda.empty_cache()
     for label, kw in DECOMP_WORKLOADS:
@@ -325,6 +368,8 @@ def profile_pass(manifest_path: str, calls: int = 24, warmup: int = 4) -> int:
         torch.cuda.empty_cache()
     with open(manifest_path, "w") as f:
         json.dump({"copy_bytes": copy_bytes, "copy_calls": copy_calls,
+                   "read_bytes": read_bytes, "read_calls": read_calls, "read_kb_per_wave": read_kb,
+                   "mode": "graph" if graph else "eager",
                    "delimiter": "null_kernel", "workloads": workloads}, f, indent=1)
     return 0
 
@@ -447,7 +492,7 @@ def main(argv=None) -> int:
     from decodebench_amd.demos.llama_decode import build_config
 
     if args.profile_pass:
-        return profile_pass(args.profile_pass)
+        return profile_pass(args.profile_pass, calls=args.calls, graph=args.graph)
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1

@@ -32,7 +32,12 @@ Three rocprofv3 runs of that program feed :func:`summarize`: ``--kernel-trace``
 (durations), ``--pmc FETCH_SIZE`` and ``--pmc WRITE_SIZE`` (KiB per dispatch,
 one counter per run).  Both counters are scaled by what they read for the
 calibration copy, so ``traffic`` is in bytes of the copy's scale:
-``scale = copy_bytes / (median counter KiB of the copies * 1024)``.
+``scale = copy_bytes / (median counter KiB of the copies * 1024)``.  The
+read-only streaming probe (``read_calls`` launches over ``read_bytes``) is a
+second calibration with the kernels' own load pattern; FETCH_SIZE must give
+the same scale for both.  A fourth, optional run of the raw read-request
+counters (:data:`RAW_READ_COUNTERS`) shows why the FETCH_SIZE scale is not 1
+(:func:`request_bytes`).
 
     python -m decodebench_amd.rocprof --manifest M.json --trace T.csv \\
         --fetch F.csv --write W.csv --md out.md --json out.json
@@ -54,7 +59,16 @@ from pathlib import Path
 
 LIB_TAG = "dbk::"
 COPY_TAG = "copyBuffer"
+READ_TAG = "stream_read_kernel"
 DELIM_TAG = "null_kernel"
+# The copy and the read-only probe must give one bytes-per-unit scale for a
+# counter to within this fraction, or the profile is rejected.
+SCALE_AGREEMENT = 0.05
+# Raw L2->memory read-request counters (one rocprofv3 --pmc run): requests of
+# any size, of 32 bytes, counted as 128-byte by the FETCH_SIZE formula
+# (TCC_BUBBLE), and of 128 bytes as gfx950 reports them.
+RAW_READ_COUNTERS = ("TCC_EA0_RDREQ_sum", "TCC_EA0_RDREQ_32B_sum", "TCC_BUBBLE_sum",
+                     "TCC_EA0_RDREQ_128B_sum")
 
 
 @dataclass
@@ -166,11 +180,12 @@ def split_workloads(dispatches: list[Dispatch], manifest: dict) -> dict[str, lis
     """Assign the dispatches to the manifest's workloads.
 
     With a ``delimiter`` in the manifest, see :func:`split_segments`;
-    otherwise the library's dispatches are taken in launch order.
+    otherwise the library's dispatches (less the read-probe calibration) are
+    taken in launch order.
     Returns ``{label: [[dispatches of call 0], [call 1], ...]}``."""
     if manifest.get("delimiter"):
         return split_segments(dispatches, manifest)
-    ours = [d for d in dispatches if LIB_TAG in d.name]
+    ours = [d for d in dispatches if LIB_TAG in d.name and READ_TAG not in d.name]
     need = sum(w["calls"] * w["kernels_per_call"] for w in manifest["workloads"])
     if len(ours) != need:
         raise ValueError(f"profile has {len(ours)} library dispatches, manifest expects {need}")
@@ -196,9 +211,38 @@ def copy_scale(dispatches: list[Dispatch], manifest: dict, counter: str) -> floa
     return manifest["copy_bytes"] / (kib * 1024.0)
 
 
-def summarize(manifest: dict, trace=None, fetch=None, write=None) -> dict:
-    """Per-workload median kernel duration and scaled HBM traffic per call."""
-    res: dict = {"copy_bytes": manifest["copy_bytes"], "workloads": {}}
+def read_scale(dispatches: list[Dispatch], manifest: dict, counter: str) -> float:
+    """Bytes per counter unit, from the read-only probe's calibration launches."""
+    reads = [d for d in dispatches if READ_TAG in d.name][: manifest["read_calls"]]
+    if len(reads) < manifest["read_calls"]:
+        raise ValueError(f"{counter}: read-probe calibration launches missing from the profile")
+    kib = statistics.median(d.counters[counter] for d in reads)
+    if kib <= 0:
+        raise ValueError(f"{counter}: read-probe calibration reads {kib} units")
+    return manifest["read_bytes"] / (kib * 1024.0)
+
+
+def request_bytes(c: dict) -> dict:
+    """Bytes read from memory per request size from the raw counters of one
+    dispatch (or a sum of them): 128-byte requests as gfx950 counts them
+    (TCC_EA0_RDREQ_128B), 32-byte ones, and the rest of TCC_EA0_RDREQ as
+    64-byte; plus what the FETCH_SIZE formula makes of the same counters
+    (it takes 128-byte requests from TCC_BUBBLE)."""
+    rd, r32 = c["TCC_EA0_RDREQ_sum"], c["TCC_EA0_RDREQ_32B_sum"]
+    bub, r128 = c["TCC_BUBBLE_sum"], c["TCC_EA0_RDREQ_128B_sum"]
+    return {"requests": rd, "req_32B": r32, "req_128B": r128, "bubble": bub,
+            "bytes_by_size": 128 * r128 + 64 * (rd - r128 - r32) + 32 * r32,
+            "fetch_size_formula_bytes": 128 * bub + 64 * (rd - bub - r32) + 32 * r32}
+
+
+def summarize(manifest: dict, trace=None, fetch=None, write=None, raw=None) -> dict:
+    """Per-workload median kernel duration and scaled HBM traffic per call.
+
+    With ``raw`` (a run of :data:`RAW_READ_COUNTERS`), the read requests of
+    the calibration kernels and of every workload are broken down by size
+    (:func:`request_bytes`)."""
+    res: dict = {"copy_bytes": manifest["copy_bytes"], "mode": manifest.get("mode", "eager"),
+                 "workloads": {}}
     per: dict[str, dict] = {w["label"]: {"algorithmic_bytes": w["algorithmic_bytes"]}
                             for w in manifest["workloads"]}
     warm = {w["label"]: w.get("warmup", 0) for w in manifest["workloads"]}
@@ -226,6 +270,13 @@ def summarize(manifest: dict, trace=None, fetch=None, write=None) -> dict:
             continue
         scale = copy_scale(disp, manifest, counter)
         res[f"{counter}_scale"] = scale
+        if manifest.get("read_calls") and counter == "FETCH_SIZE":
+            rscale = read_scale(disp, manifest, counter)
+            res[f"{counter}_read_scale"] = rscale
+            if abs(rscale / scale - 1.0) > SCALE_AGREEMENT:
+                raise ValueError(f"{counter}: the copy gives {scale:.3f} bytes per unit but the "
+                                 f"read-only probe {rscale:.3f}; the counter's unit depends on "
+                                 "the access pattern, so its traffic figures cannot be trusted")
         cw = split_workloads(disp, manifest)
         for label, calls in cw.items():
             calls = calls[warm[label]:]
@@ -233,6 +284,27 @@ def summarize(manifest: dict, trace=None, fetch=None, write=None) -> dict:
                 raise ValueError(f"{label}: no calls left after {warm[label]} warm-up calls")
             per[label][key] = statistics.median(
                 sum(d.counters[counter] for d in c) * 1024.0 * scale for c in calls)
+    if raw is not None:
+        def per_call(calls):
+            tot = {k: statistics.median(sum(d.counters.get(k, 0.0) for d in c) for c in calls)
+                   for k in RAW_READ_COUNTERS}
+            return request_bytes(tot)
+
+        calib = {}
+        copies = [d for d in raw if COPY_TAG in d.name][: manifest["copy_calls"]]
+        if copies:
+            calib["copy"] = per_call([[d] for d in copies])
+            calib["copy"]["bytes_read"] = manifest["copy_bytes"]
+        if manifest.get("read_calls"):
+            reads = [d for d in raw if READ_TAG in d.name][: manifest["read_calls"]]
+            if reads:
+                calib["read_probe"] = per_call([[d] for d in reads])
+                calib["read_probe"]["bytes_read"] = manifest["read_bytes"]
+        res["raw_read_requests"] = calib
+        for label, calls in split_workloads(raw, manifest).items():
+            calls = calls[warm[label]:]
+            if calls:
+                per[label]["read_requests"] = per_call(calls)
     for label, p in per.items():
         if "fetch_bytes" in p and "write_bytes" in p:
             p["traffic_bytes"] = p["fetch_bytes"] + p["write_bytes"]
@@ -249,6 +321,25 @@ def to_markdown(res: dict, command: str) -> str:
                      f"FETCH_SIZE x {res['FETCH_SIZE_scale']:.3f} and WRITE_SIZE x "
                      f"{res.get('WRITE_SIZE_scale', float('nan')):.3f} bytes per KiB-unit "
                      "(factors applied below).")
+        if "FETCH_SIZE_read_scale" in res:
+            lines.append(f"The read-only streaming probe (`db_stream_read`, 16-byte non-temporal "
+                         f"loads) gives FETCH_SIZE x {res['FETCH_SIZE_read_scale']:.3f}; the "
+                         f"pipeline rejects a profile where the two differ by more than "
+                         f"{SCALE_AGREEMENT:.0%}.")
+        lines.append("")
+    if res.get("raw_read_requests"):
+        lines += ["Read requests from L2 to memory by size (raw counters, one run; per "
+                  "calibration kernel or per call):", "",
+                  "| Kernel / workload | requests | 32 B | 128 B (TCC_EA0_RDREQ_128B) | "
+                  "TCC_BUBBLE | bytes by size | FETCH_SIZE formula bytes | bytes read |",
+                  "|---|---|---|---|---|---|---|---|"]
+        rows = list(res["raw_read_requests"].items()) + [
+            (k, p["read_requests"]) for k, p in res["workloads"].items() if "read_requests" in p]
+        for label, r in rows:
+            lines.append(f"| {label} | {r['requests']:,.0f} | {r['req_32B']:,.0f} | "
+                         f"{r['req_128B']:,.0f} | {r['bubble']:,.0f} | "
+                         f"{r['bytes_by_size']:,.0f} | {r['fetch_size_formula_bytes']:,.0f} | "
+                         + (f"{r['bytes_read']:,}" if "bytes_read" in r else "") + " |")
         lines.append("")
     if any(p.get("kind") == "unfused" for p in res["workloads"].values()):
         lines.append("Rows ending in `_unfused` are the torch stage chain of the same config "
@@ -266,12 +357,15 @@ def to_markdown(res: dict, command: str) -> str:
                            for k, v in p.get("kernel_us", {}).items())
         call = p.get("call_us")
         gbs = p.get("GB/s")
-        lines.append(
-            f"| {label} | {ku} | {call:.2f} | {p['algorithmic_bytes']:,} | {gbs:.0f} | "
-            f"{gbs / 80:.1f} | {p.get('fetch_bytes', float('nan')):,.0f} | "
-            f"{p.get('write_bytes', float('nan')):,.0f} | "
-            f"{p.get('traffic_over_algorithmic', float('nan')):.3f} |"
-            if call is not None else f"| {label} | | | {p['algorithmic_bytes']:,} | | | | | |")
+
+        def num(key, fmt):
+            return format(p[key], fmt) if key in p else ""
+
+        timing = (f"{ku} | {call:.2f} | {p['algorithmic_bytes']:,} | {gbs:.0f} | "
+                  f"{gbs / 80:.1f}" if call is not None
+                  else f" | | {p['algorithmic_bytes']:,} | | ")
+        lines.append(f"| {label} | {timing} | {num('fetch_bytes', ',.0f')} | "
+                     f"{num('write_bytes', ',.0f')} | {num('traffic_over_algorithmic', '.3f')} |")
     return "\n".join(lines) + "\n"
 
 
@@ -281,6 +375,7 @@ def main(argv=None) -> int:
     ap.add_argument("--trace")
     ap.add_argument("--fetch")
     ap.add_argument("--write")
+    ap.add_argument("--raw", help="counter CSV of a run of the raw read-request counters")
     ap.add_argument("--md")
     ap.add_argument("--json")
     ap.add_argument("--command", default="", help="command line recorded in the markdown")
@@ -289,7 +384,8 @@ def main(argv=None) -> int:
     res = summarize(manifest,
                     trace=read_trace(args.trace) if args.trace else None,
                     fetch=read_counters(args.fetch) if args.fetch else None,
-                    write=read_counters(args.write) if args.write else None)
+                    write=read_counters(args.write) if args.write else None,
+                    raw=read_counters(args.raw) if args.raw else None)
     if args.json:
         Path(args.json).write_text(json.dumps(res, indent=1, sort_keys=True) + "\n")
     text = to_markdown(res, args.command)

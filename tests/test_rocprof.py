@@ -187,3 +187,54 @@ def test_segments_fail_closed(tmp_path):
     trace, _, _ = _write_rows(tmp_path, SEG_ROWS)
     with pytest.raises(ValueError, match="kernels per call"):
         rocprof.summarize(bad, trace=trace)
+
+
+def _counter_csv(path, rows):
+    """rows: (name, {counter: value}) per dispatch."""
+    with open(path, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Dispatch_Id", "Grid_Size", "Kernel_Name", "Workgroup_Size",
+                    "Counter_Name", "Counter_Value"])
+        for i, (name, cs) in enumerate(rows, start=1):
+            for c, v in cs.items():
+                w.writerow([i, 256, name, 256, c, v])
+
+
+READ_MANIFEST = {"copy_bytes": 1 << 20, "copy_calls": 1, "read_bytes": 1 << 20, "read_calls": 1,
+                 "workloads": [{"label": "gemv", "calls": 1, "warmup": 0,
+                                "kernels_per_call": 1, "algorithmic_bytes": 1000}]}
+COPY = "__amd_rocclr_copyBuffer"
+PROBE = "void dbk::(anonymous namespace)::stream_read_kernel<4>(args)"
+GEMV = "void dbk::(anonymous namespace)::gemv_kernel<1>(args)"
+
+
+def test_read_probe_scale_must_agree_with_the_copy(tmp_path):
+    ok = [(COPY, {"FETCH_SIZE": 512.0}), (PROBE, {"FETCH_SIZE": 520.0}),
+          (GEMV, {"FETCH_SIZE": 1.0})]
+    _counter_csv(tmp_path / "ok.csv", ok)
+    res = rocprof.summarize(READ_MANIFEST, fetch=rocprof.read_counters(tmp_path / "ok.csv"))
+    assert res["FETCH_SIZE_scale"] == pytest.approx(2.0)
+    assert res["FETCH_SIZE_read_scale"] == pytest.approx(1024 / 520)
+    # a counter whose unit changes with the access pattern is rejected
+    bad = [(COPY, {"FETCH_SIZE": 512.0}), (PROBE, {"FETCH_SIZE": 1024.0}),
+           (GEMV, {"FETCH_SIZE": 1.0})]
+    _counter_csv(tmp_path / "bad.csv", bad)
+    with pytest.raises(ValueError, match="read-only probe"):
+        rocprof.summarize(READ_MANIFEST, fetch=rocprof.read_counters(tmp_path / "bad.csv"))
+
+
+def test_raw_read_requests_by_size(tmp_path):
+    # 1 MiB read as 8192 requests of 128 bytes, all reported in TCC_EA0_RDREQ_128B and none
+    # in TCC_BUBBLE: bytes by size are exact, the FETCH_SIZE formula counts them as 64 bytes.
+    req = {"TCC_EA0_RDREQ_sum": 8192, "TCC_EA0_RDREQ_32B_sum": 0, "TCC_BUBBLE_sum": 0,
+           "TCC_EA0_RDREQ_128B_sum": 8192}
+    mix = {"TCC_EA0_RDREQ_sum": 10, "TCC_EA0_RDREQ_32B_sum": 2, "TCC_BUBBLE_sum": 3,
+           "TCC_EA0_RDREQ_128B_sum": 5}
+    _counter_csv(tmp_path / "raw.csv", [(COPY, req), (PROBE, req), (GEMV, mix)])
+    res = rocprof.summarize(READ_MANIFEST, raw=rocprof.read_counters(tmp_path / "raw.csv"))
+    probe = res["raw_read_requests"]["read_probe"]
+    assert probe["bytes_by_size"] == 1 << 20
+    assert probe["fetch_size_formula_bytes"] == (1 << 20) // 2
+    g = res["workloads"]["gemv"]["read_requests"]
+    assert g["bytes_by_size"] == 128 * 5 + 64 * 3 + 32 * 2
+    assert g["fetch_size_formula_bytes"] == 128 * 3 + 64 * 5 + 32 * 2
