@@ -12,6 +12,9 @@ the 256 MB Infinity Cache), so every step streams its weights from HBM.
   roofline       the F2 kernel against the 8 TB/s HBM3E peak; its average
                  launch duration is the same event-timed region on the
                  stream the kernel runs on (torch's current stream)
+  roofline_by_kernel  F1 (configs 1 and 3), F2 and F4 (L = 8192, 32768) at
+                 batch 1 against the 8 TB/s peak, from the kernels table, with
+                 the committed rocprofv3 kernel-trace medians beside them
   kernels        F1 (config 1 and the QKV shape of config 3), F2 and F4
                  (config 4 at L = 1024 / 8192 / 32768) with their batch and
                  split sweeps, the fp8 e4m3-weight F1/F2 and the config-5
@@ -82,16 +85,31 @@ def parse_args(argv=None):
                          "decomposition and the CPU baseline")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.json"),
                     help="rocprofv3 traffic summary (decodebench_amd.rocprof) for roofline.traffic")
+    ap.add_argument("--kernel-trace", default=os.path.join(ROOT, "profiles",
+                                                           "kernel_trace_b1.json"),
+                    help="rocprofv3 graph-replay kernel-trace summary for roofline_by_kernel")
     return ap.parse_args(argv)
 
 
 # ----------------------------------------------------------------- timing
-def time_steps(case, steps: int, warmup: int):
-    """Eager launches, one per step, replica i % n; returns seconds."""
+def time_steps(case, steps: int, warmup: int, settle_ms: float = 20.0):
+    """Eager launches, one per step, replica i % n; returns seconds.
+
+    Before the ``warmup`` steps the GPU is kept busy with about ``settle_ms``
+    of the same launches (untimed, not counted as steps), so that a short
+    timed region (the driver's 20 steps are 0.7 ms) does not start while the
+    clocks are still ramping up from the parity check."""
     import torch
 
     reps = case.replicas
     n = len(reps)
+    t0 = time.perf_counter()
+    i = 0
+    while (time.perf_counter() - t0) * 1e3 < settle_ms:
+        case.fused(reps[i % n])
+        i += 1
+        if i % 64 == 0:
+            torch.cuda.synchronize()
     for i in range(warmup):
         case.fused(reps[i % n])
     torch.cuda.synchronize()
@@ -150,19 +168,25 @@ def time_graph_launches(case, min_launches: int = 96, replays: int = 20):
 
 
 CHECK_REL_L2 = 1e-2
+# The decode-layer chain compounds twelve fp16 rounding points; two correct
+# implementations of it differ by up to 1.6e-2 elementwise, so it is held to
+# the parity tests' chain tolerance (each of its kernels meets 1e-2 alone).
+CHECK_TOL = {"layer": 2e-2}
 
 
 def check_case(case) -> float:
     """Fused output vs the unfused torch stages on the GPU: rtol/atol 1e-2
-    elementwise, and relative L2 <= 1e-2, which an all-zero output fails
-    also where |o| is below atol (F4 at long KV lengths)."""
+    elementwise (2e-2 for the decode-layer chain), and relative L2 <= 1e-2,
+    which an all-zero output fails also where |o| is below atol (F4 at long
+    KV lengths)."""
     import torch
 
     ref = case.seq._replay_body(case.inputs).float()
     out = case.fused(case.inputs).float()
     torch.cuda.synchronize()
     err = float((out - ref).norm() / ref.norm().clamp_min(1e-30))
-    if not torch.allclose(out, ref, rtol=1e-2, atol=1e-2) or not err <= CHECK_REL_L2:
+    tol = CHECK_TOL.get(case.name, 1e-2)
+    if not torch.allclose(out, ref, rtol=tol, atol=tol) or not err <= CHECK_REL_L2:
         raise RuntimeError(f"{case.name}: fused output differs from the torch stages "
                            f"(max abs {float((out - ref).abs().max()):.3e}, rel-L2 {err:.3e})")
     return err
@@ -374,6 +398,50 @@ def profile_pass(manifest_path: str, calls: int = 24, warmup: int = 4,
     return 0
 
 
+# The batch-1 kernels the metric names (F1 at configs 1 and 3, F2, F4), with the
+# kernel names of their launches.
+ROOFLINE_KERNELS = (("f1_cfg1", "gemv_kernel<1,...> (F1 RMSNorm mode)"),
+                    ("f1_qkv_cfg3", "gemv_kernel<1,...> (F1 RMSNorm mode)"),
+                    ("f2_cfg2", "gemv_kernel<2,...> (F2 SwiGLU mode)"),
+                    ("f4_L8192", "f4_kernel<4,8,...> + f4_combine"),
+                    ("f4_L32768", "f4_kernel<4,8,...> + f4_combine"))
+
+
+def load_kernel_trace(path: str) -> dict:
+    try:
+        with open(path) as f:
+            return json.load(f).get("workloads", {})
+    except (OSError, ValueError):
+        return {}
+
+
+def roofline_by_kernel(kernels: dict, traffic: dict, trace: dict) -> dict:
+    """Per batch-1 kernel: algorithmic bytes / its average launch time
+    against 8 TB/s.  ``us`` is this run's event-timed average over
+    back-to-back launches replayed from a hipGraph; ``rocprof_us`` is the
+    committed rocprofv3 kernel-trace median of the same calls replayed the
+    same way (profiles/kernel_trace_b1.md, profiler overhead included);
+    ``traffic`` the committed FETCH_SIZE + WRITE_SIZE bytes per call."""
+    out = {}
+    for name, kernel in ROOFLINE_KERNELS:
+        k = kernels.get(name)
+        if not k:
+            continue
+        achieved = k["GB/s"]
+        row = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+               "frac": round(achieved / HBM_PEAK_GBS, 4), "us": k["us"],
+               "algorithmic_bytes": k["algorithmic_bytes"], "kernel": kernel,
+               "traffic": traffic.get(name, {}).get("traffic_bytes"),
+               "bar_70pct_us": round(k["algorithmic_bytes"] / (0.7 * HBM_PEAK_GBS * 1e3), 3)}
+        t = trace.get(name, {})
+        if "call_us" in t:
+            row["rocprof_us"] = round(t["call_us"], 3)
+            row["rocprof_kernel_us"] = {kk.split("::")[-1]: round(v, 3)
+                                        for kk, v in t.get("kernel_us", {}).items()}
+        out[name] = row
+    return out
+
+
 def load_traffic(path: str) -> dict:
     try:
         with open(path) as f:
@@ -550,6 +618,8 @@ def main(argv=None) -> int:
             del case
             torch.cuda.empty_cache()
         out["kernels"] = kernels
+        out["roofline_by_kernel"] = roofline_by_kernel(kernels, traffic,
+                                                       load_kernel_trace(args.kernel_trace))
 
     if not args.quick and not args.sweep_only:
         # ---- Delta_launch vs B: unfused stream / graph vs fused ----------
@@ -560,11 +630,16 @@ def main(argv=None) -> int:
                                    warmup=10, input_replicas=case.replicas,
                                    fused=case.fused)
             v = rep.verdict()
+            # the fused call replayed back to back from a graph, as the unfused
+            # chain's t_graph is: the residual against it holds no host time
+            t_fused_graph, _ = time_graph_launches(case, replays=10)
             decomp[name] = {
                 "t_stream_us": round(v.t_stream, 3), "t_graph_us": round(v.t_graph, 3),
                 "t_fused_us": round(v.t_fused, 3), "delta_launch_us": round(v.delta_launch, 3),
                 "delta_launch_ci": [round(c, 3) for c in v.delta_launch_ci],
                 "B_us": round(v.b_bytes_est, 3), "residual_us": round(v.residual_us, 3),
+                "t_fused_graph_us": round(t_fused_graph, 3),
+                "residual_graph_us": round(v.t_graph - t_fused_graph - v.b_bytes_est, 3),
                 "bound": v.bound, "dominant": v.dominant,
                 "total_bytes": v.total_bytes, "eliminable_bytes": v.eliminable_bytes,
                 "fused_extra_bytes": f4_partial_bytes(kw),
@@ -572,7 +647,8 @@ def main(argv=None) -> int:
                 "samples_us": {k: [round(t, 3) for t in getattr(rep, f"{k}_us")]
                                for k in ("stream", "graph", "fused")}}
             log(f"{name}: stream {v.t_stream:.2f} graph {v.t_graph:.2f} fused "
-                f"{v.t_fused:.2f} us; dL {v.delta_launch:.2f} B {v.b_bytes_est:.3f}")
+                f"{v.t_fused:.2f} (graph {t_fused_graph:.2f}) us; dL {v.delta_launch:.2f} "
+                f"B {v.b_bytes_est:.3f}")
             del case, rep
             torch.cuda.empty_cache()
         out["decomposition"] = decomp

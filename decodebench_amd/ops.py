@@ -17,7 +17,6 @@ ops raise ``RuntimeError`` naming the build command.
 
 from __future__ import annotations
 
-import contextlib
 import ctypes as C
 import math
 import threading
@@ -98,25 +97,6 @@ def _check(rc: int, what: str) -> None:
     raise RuntimeError(f"{what} failed (HIP error {rc}): {msg}")
 
 
-def _stream_ptr(t) -> int:
-    import torch
-
-    return torch.cuda.current_stream(t.device).cuda_stream
-
-
-def _require(t, name: str, dtype=None) -> None:
-    import torch
-
-    if not isinstance(t, torch.Tensor):
-        raise TypeError(f"{name} must be a torch.Tensor")
-    if t.device.type != "cuda":
-        raise ValueError(f"{name} must be on a GPU device (got {t.device})")
-    if dtype is not None and t.dtype != dtype:
-        raise TypeError(f"{name} must be {dtype} (got {t.dtype})")
-    if not t.is_contiguous():
-        raise ValueError(f"{name} must be contiguous")
-
-
 def _same_device(*named) -> None:
     """All tensors of one call must live on one GPU."""
     dev = named[0][0].device
@@ -125,22 +105,83 @@ def _same_device(*named) -> None:
             raise ValueError(f"{name} is on {t.device}, expected {dev} like {named[0][1]}")
 
 
-def _on_device(t):
-    """Make t's GPU current for the library call (its launches and CU-count
-    query use the current HIP device); a no-op when it already is."""
-    import torch
+_torch = None
+_raw_stream = None
 
-    idx = t.device.index
-    if idx is None or idx == torch.cuda.current_device():
-        return contextlib.nullcontext()
-    return torch.cuda.device(idx)
+
+def _torch_mod():
+    """torch, imported once, and the fastest handle to the current stream."""
+    global _torch, _raw_stream
+    if _torch is None:
+        import torch
+
+        raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+        _raw_stream = raw if raw is not None else (
+            lambda idx: torch.cuda.current_stream(idx).cuda_stream)
+        _torch = torch
+    return _torch
+
+
+def _gpu_tensors(*items) -> int:
+    """Check ``(tensor, name, dtype or None)`` items in one pass: a torch
+    tensor on a GPU, of that dtype, contiguous, all on one GPU.  Returns the
+    GPU's index.  Every check is a C-level attribute read, so the hot call
+    stays cheap."""
+    torch = _torch or _torch_mod()
+    idx, first = -1, None
+    for t, name, dt in items:
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a torch.Tensor")
+        if not t.is_cuda:
+            raise ValueError(f"{name} must be on a GPU device (got {t.device})")
+        if dt is not None and t.dtype != dt:
+            raise TypeError(f"{name} must be {dt} (got {t.dtype})")
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+        d = t.get_device()
+        if first is None:
+            idx, first = d, name
+        elif d != idx:
+            raise ValueError(f"{name} is on cuda:{d}, expected cuda:{idx} like {first}")
+    return idx
+
+
+def _launch(fn, idx: int, what: str, *args) -> None:
+    """``fn(*args, stream)`` on GPU ``idx`` (made current if it is not) and
+    its current stream; a non-zero status raises."""
+    torch = _torch
+    if torch.cuda.current_device() == idx:
+        rc = fn(*args, _raw_stream(idx))
+    else:
+        with torch.cuda.device(idx):
+            rc = fn(*args, _raw_stream(idx))
+    if rc:
+        _check(rc, what)
+
+
+def _output(shape, idx: int, out, name: str = "out"):
+    """A new fp16 tensor of ``shape`` on GPU ``idx``, or ``out`` checked."""
+    torch = _torch
+    if out is None:
+        return torch.empty(shape, dtype=torch.float16, device=torch.device("cuda", idx))
+    _gpu_tensors((out, name, torch.float16))
+    if out.get_device() != idx:
+        raise ValueError(f"{name} is on cuda:{out.get_device()}, expected cuda:{idx}")
+    if tuple(out.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)} (got {tuple(out.shape)})")
+    return out
 
 
 def cu_count(device=None) -> int:
-    import torch
-
-    dev = torch.device("cuda" if device is None else device)
-    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    """Compute units of a GPU (index, torch.device or None for the current one)."""
+    if isinstance(device, int) and device in _cu_cache:
+        return _cu_cache[device]
+    torch = _torch or _torch_mod()
+    if isinstance(device, int):
+        idx = device
+    else:
+        dev = torch.device("cuda" if device is None else device)
+        idx = dev.index if dev.index is not None else torch.cuda.current_device()
     if idx not in _cu_cache:
         _cu_cache[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
     return _cu_cache[idx]
@@ -167,14 +208,12 @@ def stream_read(src, kb_per_wave: int = 8, sink=None) -> None:
     given; pass one to keep the call allocation-free (graph capture)."""
     import torch
 
-    _require(src, "src")
+    idx = _gpu_tensors((src, "src", None))
     nbytes = src.numel() * src.element_size()
     if sink is None:
-        sink = torch.empty(max(1, nbytes // 16), dtype=torch.int32, device=src.device)
-    with _on_device(src):
-        rc = load_library().db_stream_read(src.data_ptr(), nbytes, int(kb_per_wave), 0x9E3779B9,
-                                           sink.data_ptr(), _stream_ptr(src))
-    _check(rc, "db_stream_read")
+        sink = _torch.empty(max(1, nbytes // 16), dtype=_torch.int32, device=src.device)
+    _launch((_lib or load_library()).db_stream_read, idx, "db_stream_read", src.data_ptr(),
+            nbytes, int(kb_per_wave), 0x9E3779B9, sink.data_ptr())
 
 
 def tune(key: str, value: int) -> None:
@@ -184,20 +223,19 @@ def tune(key: str, value: int) -> None:
 
 
 def _weights(W, w_scale, name: str, N: int, K: int):
-    """(dtype code, scale pointer) for an fp16 or e4m3 weight matrix."""
-    import torch
-
+    """(dtype code, scale pointer, items to check) for an fp16 or e4m3 weight
+    matrix."""
+    torch = _torch or _torch_mod()
     if W.dtype == torch.float16:
         if w_scale is not None:
             raise ValueError(f"{name}: fp16 weights take no scale")
-        return DTYPE_F16, None
+        return DTYPE_F16, None, ()
     if W.dtype in (torch.float8_e4m3fn, torch.uint8):
         if w_scale is None:
             raise ValueError(f"{name}: fp8 weights need a per-row fp32 scale")
-        _require(w_scale, f"{name} scale", torch.float32)
-        if tuple(w_scale.shape) != (N,):
-            raise ValueError(f"{name} scale must have shape ({N},)")
-        return DTYPE_FP8_E4M3, w_scale.data_ptr()
+        if not isinstance(w_scale, torch.Tensor) or tuple(w_scale.shape) != (N,):
+            raise ValueError(f"{name} scale must be a tensor of shape ({N},)")
+        return DTYPE_FP8_E4M3, w_scale.data_ptr(), ((w_scale, f"{name} scale", torch.float32),)
     raise TypeError(f"{name}: unsupported weight dtype {W.dtype}")
 
 
@@ -209,74 +247,55 @@ def _as_2d(x, name: str):
     return x, False
 
 
-def f1_rmsnorm_gemv(x, g, W, eps: float = 1e-6, w_scale=None):
+def f1_rmsnorm_gemv(x, g, W, eps: float = 1e-6, w_scale=None, out=None):
     """F1: ``F.linear(rmsnorm(x, g, eps), W)`` in one kernel.
 
     x [B,K] (or [K]) fp16, g [K] fp16, W [N,K] fp16 (or e4m3 + w_scale [N]).
-    Returns [B,N] fp16 (or [N] for a 1-D x)."""
-    import torch
-
-    _require(x, "x", torch.float16)
-    _require(g, "g", torch.float16)
-    _require(W, "W")
+    Returns [B,N] fp16 (or [N] for a 1-D x), written to ``out`` if given."""
+    torch = _torch or _torch_mod()
     x2, squeeze = _as_2d(x, "x")
     B, K = x2.shape
     if W.dim() != 2 or W.shape[1] != K or g.shape != (K,):
         raise ValueError(f"shape mismatch: x {tuple(x.shape)}, g {tuple(g.shape)}, "
                          f"W {tuple(W.shape)}")
     N = W.shape[0]
-    dt, sp = _weights(W, w_scale, "W", N, K)
-    _same_device((x, "x"), (g, "g"), (W, "W"), *(((w_scale, "w_scale"),) if sp else ()))
-    y = torch.empty((B, N), dtype=torch.float16, device=x.device)
-    with _on_device(x):
-        rc = load_library().db_f1_rmsnorm_gemv(x2.data_ptr(), g.data_ptr(), W.data_ptr(), sp,
-                                               y.data_ptr(), B, K, N, float(eps), dt,
-                                               _stream_ptr(x))
-    _check(rc, "db_f1_rmsnorm_gemv")
+    dt, sp, sc = _weights(W, w_scale, "W", N, K)
+    idx = _gpu_tensors((x, "x", torch.float16), (g, "g", torch.float16), (W, "W", None), *sc)
+    y = _output((B, N), idx, out)
+    _launch((_lib or load_library()).db_f1_rmsnorm_gemv, idx, "db_f1_rmsnorm_gemv",
+            x2.data_ptr(), g.data_ptr(), W.data_ptr(), sp, y.data_ptr(), B, K, N,
+            float(eps), dt)
     return y[0] if squeeze else y
 
 
-def f2_gateup_swiglu(x, Wg, Wu, sg=None, su=None):
+def f2_gateup_swiglu(x, Wg, Wu, sg=None, su=None, out=None):
     """F2: ``silu(F.linear(x, Wg)) * F.linear(x, Wu)`` in one kernel.
 
     x [B,K] (or [K]) fp16, Wg/Wu [N,K] fp16 (or e4m3 + per-row scales)."""
-    import torch
-
-    _require(x, "x", torch.float16)
-    _require(Wg, "Wg")
-    _require(Wu, "Wu")
+    torch = _torch or _torch_mod()
     x2, squeeze = _as_2d(x, "x")
     B, K = x2.shape
     if Wg.dim() != 2 or Wg.shape != Wu.shape or Wg.shape[1] != K or Wg.dtype != Wu.dtype:
         raise ValueError(f"shape mismatch: x {tuple(x.shape)}, Wg {tuple(Wg.shape)}, "
                          f"Wu {tuple(Wu.shape)}")
     N = Wg.shape[0]
-    dt, sgp = _weights(Wg, sg, "Wg", N, K)
-    _, sup = _weights(Wu, su, "Wu", N, K)
-    _same_device((x, "x"), (Wg, "Wg"), (Wu, "Wu"),
-                 *(((sg, "sg"), (su, "su")) if sgp else ()))
-    y = torch.empty((B, N), dtype=torch.float16, device=x.device)
-    with _on_device(x):
-        rc = load_library().db_f2_gateup_swiglu(x2.data_ptr(), Wg.data_ptr(), Wu.data_ptr(),
-                                                sgp, sup, y.data_ptr(), B, K, N, dt,
-                                                _stream_ptr(x))
-    _check(rc, "db_f2_gateup_swiglu")
+    dt, sgp, sgc = _weights(Wg, sg, "Wg", N, K)
+    _, sup, suc = _weights(Wu, su, "Wu", N, K)
+    idx = _gpu_tensors((x, "x", torch.float16), (Wg, "Wg", None), (Wu, "Wu", None), *sgc, *suc)
+    y = _output((B, N), idx, out)
+    _launch((_lib or load_library()).db_f2_gateup_swiglu, idx, "db_f2_gateup_swiglu",
+            x2.data_ptr(), Wg.data_ptr(), Wu.data_ptr(), sgp, sup, y.data_ptr(), B, K, N, dt)
     return y[0] if squeeze else y
 
 
-def f2_rmsnorm_gateup_swiglu(x, g, Wg, Wu, eps: float = 1e-6, sg=None, su=None):
+def f2_rmsnorm_gateup_swiglu(x, g, Wg, Wu, eps: float = 1e-6, sg=None, su=None, out=None):
     """RMSNorm -> F2 in one kernel: ``f2_gateup_swiglu(rmsnorm(x, g, eps), Wg, Wu)``
     with the normalised activations kept on chip (the post-attention half
     of the decode-layer chain).
 
     x [B,K] (or [K]) fp16, g [K] fp16, Wg/Wu [N,K] fp16 (or e4m3 + per-row
     scales).  Returns [B,N] fp16 (or [N])."""
-    import torch
-
-    _require(x, "x", torch.float16)
-    _require(g, "g", torch.float16)
-    _require(Wg, "Wg")
-    _require(Wu, "Wu")
+    torch = _torch or _torch_mod()
     x2, squeeze = _as_2d(x, "x")
     B, K = x2.shape
     if (Wg.dim() != 2 or Wg.shape != Wu.shape or Wg.shape[1] != K or Wg.dtype != Wu.dtype
@@ -284,37 +303,30 @@ def f2_rmsnorm_gateup_swiglu(x, g, Wg, Wu, eps: float = 1e-6, sg=None, su=None):
         raise ValueError(f"shape mismatch: x {tuple(x.shape)}, g {tuple(g.shape)}, "
                          f"Wg {tuple(Wg.shape)}, Wu {tuple(Wu.shape)}")
     N = Wg.shape[0]
-    dt, sgp = _weights(Wg, sg, "Wg", N, K)
-    _, sup = _weights(Wu, su, "Wu", N, K)
-    _same_device((x, "x"), (g, "g"), (Wg, "Wg"), (Wu, "Wu"),
-                 *(((sg, "sg"), (su, "su")) if sgp else ()))
-    y = torch.empty((B, N), dtype=torch.float16, device=x.device)
-    with _on_device(x):
-        rc = load_library().db_f2_rmsnorm_gateup_swiglu(
-            x2.data_ptr(), g.data_ptr(), Wg.data_ptr(), Wu.data_ptr(), sgp, sup, y.data_ptr(),
-            B, K, N, float(eps), dt, _stream_ptr(x))
-    _check(rc, "db_f2_rmsnorm_gateup_swiglu")
+    dt, sgp, sgc = _weights(Wg, sg, "Wg", N, K)
+    _, sup, suc = _weights(Wu, su, "Wu", N, K)
+    idx = _gpu_tensors((x, "x", torch.float16), (g, "g", torch.float16), (Wg, "Wg", None),
+                       (Wu, "Wu", None), *sgc, *suc)
+    y = _output((B, N), idx, out)
+    _launch((_lib or load_library()).db_f2_rmsnorm_gateup_swiglu, idx,
+            "db_f2_rmsnorm_gateup_swiglu", x2.data_ptr(), g.data_ptr(), Wg.data_ptr(),
+            Wu.data_ptr(), sgp, sup, y.data_ptr(), B, K, N, float(eps), dt)
     return y[0] if squeeze else y
 
 
-def gemv(x, W, w_scale=None):
+def gemv(x, W, w_scale=None, out=None):
     """Plain projection ``F.linear(x, W)`` (fp16 out, fp32 accumulation)."""
-    import torch
-
-    _require(x, "x", torch.float16)
-    _require(W, "W")
+    torch = _torch or _torch_mod()
     x2, squeeze = _as_2d(x, "x")
     B, K = x2.shape
     if W.dim() != 2 or W.shape[1] != K:
         raise ValueError(f"shape mismatch: x {tuple(x.shape)}, W {tuple(W.shape)}")
     N = W.shape[0]
-    dt, sp = _weights(W, w_scale, "W", N, K)
-    _same_device((x, "x"), (W, "W"), *(((w_scale, "w_scale"),) if sp else ()))
-    y = torch.empty((B, N), dtype=torch.float16, device=x.device)
-    with _on_device(x):
-        rc = load_library().db_gemv(x2.data_ptr(), W.data_ptr(), sp, y.data_ptr(), B, K, N, dt,
-                                    _stream_ptr(x))
-    _check(rc, "db_gemv")
+    dt, sp, sc = _weights(W, w_scale, "W", N, K)
+    idx = _gpu_tensors((x, "x", torch.float16), (W, "W", None), *sc)
+    y = _output((B, N), idx, out)
+    _launch((_lib or load_library()).db_gemv, idx, "db_gemv",
+            x2.data_ptr(), W.data_ptr(), sp, y.data_ptr(), B, K, N, dt)
     return y[0] if squeeze else y
 
 
@@ -380,16 +392,13 @@ def release_captured_workspaces() -> int:
 
 
 def f4_flashdecode(q, K, V, scale: float | None = None, n_splits: int | None = None,
-                   workspace=None):
+                   workspace=None, out=None):
     """F4: split-KV GQA decode attention with the log-sum-exp merge.
 
     q [B,Hq,D], K/V [B,Hkv,L,D] fp16 (D = 128); query head h reads KV head
     h // (Hq // Hkv).  ``scale`` defaults to 1/sqrt(D); ``n_splits`` defaults
     to the library's CU-count-based choice.  Returns [B,Hq,D] fp16."""
-    import torch
-
-    for t, n in ((q, "q"), (K, "K"), (V, "V")):
-        _require(t, n, torch.float16)
+    torch = _torch or _torch_mod()
     if q.dim() != 3 or K.dim() != 4 or K.shape != V.shape:
         raise ValueError(f"expected q [B,Hq,D] and K, V [B,Hkv,L,D]; got q {tuple(q.shape)}, "
                          f"K {tuple(K.shape)}, V {tuple(V.shape)}")
@@ -397,20 +406,20 @@ def f4_flashdecode(q, K, V, scale: float | None = None, n_splits: int | None = N
     Bk, Hkv, L, Dk = K.shape
     if Bk != B or Dk != D:
         raise ValueError(f"q {tuple(q.shape)} and K {tuple(K.shape)} disagree on B or D")
-    _same_device((q, "q"), (K, "K"), (V, "V"),
-                 *(((workspace, "workspace"),) if workspace is not None else ()))
+    f16 = torch.float16
+    idx = _gpu_tensors((q, "q", f16), (K, "K", f16), (V, "V", f16),
+                       *(((workspace, "workspace", None),) if workspace is not None else ()))
     scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
-    S = f4_default_splits(B, Hkv, L, q.device) if n_splits is None else int(n_splits)
+    lib = _lib or load_library()
+    S = int(lib.db_f4_default_splits(B, Hkv, L, cu_count(idx))) if n_splits is None \
+        else int(n_splits)
     if workspace is None:
-        workspace = f4_workspace(B, Hq, Hkv, L, D, S, q.device)
+        workspace = f4_workspace(B, Hq, Hkv, L, D, S, idx)
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
-    o = torch.empty((B, Hq, D), dtype=torch.float16, device=q.device)
-    with _on_device(q):
-        rc = load_library().db_f4_splitkv(q.data_ptr(), K.data_ptr(), V.data_ptr(), o.data_ptr(),
-                                          ws_ptr, ws_bytes, B, Hq, Hkv, L, D, S, scale,
-                                          _stream_ptr(q))
-    _check(rc, "db_f4_splitkv")
+    o = _output((B, Hq, D), idx, out)
+    _launch(lib.db_f4_splitkv, idx, "db_f4_splitkv", q.data_ptr(), K.data_ptr(), V.data_ptr(),
+            o.data_ptr(), ws_ptr, ws_bytes, B, Hq, Hkv, L, D, S, scale)
     return o
 
 
@@ -426,10 +435,7 @@ def f4_flashdecode_noalloc(q, K, V, scale: float | None = None, n_splits: int | 
     one GPU (concurrent streams or concurrently replayed graphs) race.  Make
     the first call on a device outside graph capture (it looks up the
     array's device address)."""
-    import torch
-
-    for t, n in ((q, "q"), (K, "K"), (V, "V")):
-        _require(t, n, torch.float16)
+    torch = _torch or _torch_mod()
     if q.dim() != 3 or K.dim() != 4 or K.shape != V.shape:
         raise ValueError(f"expected q [B,Hq,D] and K, V [B,Hkv,L,D]; got q {tuple(q.shape)}, "
                          f"K {tuple(K.shape)}, V {tuple(V.shape)}")
@@ -437,18 +443,13 @@ def f4_flashdecode_noalloc(q, K, V, scale: float | None = None, n_splits: int | 
     Bk, Hkv, L, Dk = K.shape
     if Bk != B or Dk != D:
         raise ValueError(f"q {tuple(q.shape)} and K {tuple(K.shape)} disagree on B or D")
-    if out is None:
-        out = torch.empty((B, Hq, D), dtype=torch.float16, device=q.device)
-    else:
-        _require(out, "out", torch.float16)
-        if tuple(out.shape) != (B, Hq, D):
-            raise ValueError(f"out must have shape {(B, Hq, D)} (got {tuple(out.shape)})")
-    _same_device((q, "q"), (K, "K"), (V, "V"), (out, "out"))
+    f16 = torch.float16
+    idx = _gpu_tensors((q, "q", f16), (K, "K", f16), (V, "V", f16))
+    out = _output((B, Hq, D), idx, out)
     scale = 1.0 / math.sqrt(D) if scale is None else float(scale)
-    S = f4_default_splits(B, Hkv, L, q.device) if n_splits is None else int(n_splits)
-    with _on_device(q):
-        rc = load_library().db_f4_splitkv_noalloc(q.data_ptr(), K.data_ptr(), V.data_ptr(),
-                                                  out.data_ptr(), B, Hq, Hkv, L, D, S, scale,
-                                                  _stream_ptr(q))
-    _check(rc, "db_f4_splitkv_noalloc")
+    lib = _lib or load_library()
+    S = int(lib.db_f4_default_splits(B, Hkv, L, cu_count(idx))) if n_splits is None \
+        else int(n_splits)
+    _launch(lib.db_f4_splitkv_noalloc, idx, "db_f4_splitkv_noalloc", q.data_ptr(), K.data_ptr(),
+            V.data_ptr(), out.data_ptr(), B, Hq, Hkv, L, D, S, scale)
     return out
