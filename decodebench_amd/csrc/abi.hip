@@ -344,6 +344,10 @@ int db_tune(const char* key, int value) {
     if (value < 0 || value > 2)
       return fail(DB_ERR_INVALID, "db_tune: f4_line must be 0 (auto), 1 (whole lines) or 2");
     t.f4_line = value;
+  } else if (!strcmp(key, "f4_combine_groups")) {
+    if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8)
+      return fail(DB_ERR_INVALID, "db_tune: f4_combine_groups must be 0, 1, 2, 4 or 8");
+    t.f4_combine_groups = value;
   } else if (!strcmp(key, "f4_min_tiles")) {
     if (value < 1) return fail(DB_ERR_INVALID, "db_tune: f4_min_tiles must be >= 1");
     t.f4_min_tiles = value;

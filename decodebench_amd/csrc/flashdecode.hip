@@ -464,14 +464,19 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
     __hip_atomic_store(&a.ticket[pair], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Second launch of a split call: one workgroup per (pair, query head).
-// Thread (grp, d4) merges the splits grp, grp + 8, ... of float4 slot d4 by
-// online log-sum-exp in base 2 (all loads of a chunk of 8 splits are issued
-// together), then the 8 groups merge through LDS and write the fp16 output.
-// The kernel boundary orders the partial stores of the first launch before
-// these loads.
-__global__ __launch_bounds__(256) void f4_combine(F4Args a, int G) {
-  constexpr int kGroups = 8;
+// Second launch of a split call: one workgroup of kGroups x 32 threads per
+// (pair, query head).  Thread (grp, d4) merges the splits grp, grp +
+// kGroups, ... of float4 slot d4 by online log-sum-exp in base 2 (all loads
+// of a chunk of 8 splits are issued together), then the groups merge
+// through LDS and write the fp16 output.  The launcher picks kGroups so that
+// a thread's splits make one chunk, with at least one whole wave (measured on
+// MI355X, 32 q / 8 kv heads: 32 splits with 4 groups beat 8 by 0.15 us at
+// batch 1, L = 8192 and 32768; 16 or 32 groups cost 0.4-2 us; 4-8 splits run
+// best with 2 groups, 0.2-0.4 us ahead of 8; one group of 32 threads, or one
+// wave holding 16 splits per lane, lost 0.1-2 us).  The kernel boundary orders the partial stores of the first
+// launch before these loads.
+template <int kGroups>
+__global__ __launch_bounds__(kGroups * 32) void f4_combine(F4Args a, int G) {
   __shared__ float s_c[kGroups][kD / 4][6];
   // blockIdx = h * pairs + pair: with the XCD-aware numbering of the first
   // launch, the merge of a pair runs on the XCD whose L2 holds its partials.
@@ -640,7 +645,15 @@ hipError_t launch_f4(const void* q, const void* k, const void* v, void* o,
   if (a.S > 1 && !a.fused_merge) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(f4_combine, dim3(pairs * G), dim3(256), 0, stream, a, G);
+    const int forced = tuning().f4_combine_groups;
+    const int want = forced > 0 ? forced : (a.S + kMergeChunk - 1) / kMergeChunk;
+    // at least one whole wave: 32-thread workgroups measured slower
+    const int groups = want <= 1 ? (forced == 1 ? 1 : 2) : want <= 2 ? 2 : want <= 4 ? 4 : 8;
+    const auto fn = groups == 1   ? f4_combine<1>
+                    : groups == 2 ? f4_combine<2>
+                    : groups == 4 ? f4_combine<4>
+                                  : f4_combine<8>;
+    hipLaunchKernelGGL(fn, dim3(pairs * G), dim3(groups * 32), 0, stream, a, G);
   }
   return hipGetLastError();
 }

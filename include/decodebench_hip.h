@@ -199,8 +199,9 @@ int db_stream_read(const void* src, size_t bytes, int kb_per_wave, unsigned magi
  * e4m3 gate/up pair), "f4_blocks_per_cu", "f4_min_tiles",
  * "f4_waves" (4 or 8 waves per workgroup, 0: automatic), "f4_merge" (0: the
  * split merge runs in a second launch, the default; 1: in the same launch)
- * and "f4_line" (F4 score-operand layout: 0 automatic, 1 whole-line K loads,
- * 2 16 keys x 64 bytes per load).
+ * "f4_line" (F4 score-operand layout: 0 automatic, 1 whole-line K loads,
+ * 2 16 keys x 64 bytes per load) and "f4_combine_groups" (split groups of
+ * 32 threads per merge workgroup: 1, 2, 4 or 8; 0 automatic).
  * Process-wide; no counterpart in the reference. */
 int db_tune(const char* key, int value);
 
