@@ -313,9 +313,13 @@ def summarize(manifest: dict, trace=None, fetch=None, write=None, raw=None) -> d
     return res
 
 
-def to_markdown(res: dict, command: str) -> str:
-    lines = ["# Fused decode kernels on MI355X: duration and HBM traffic per call", "",
-             "Commands (repo root, one MI355X):", "", "```", command.strip(), "```", ""]
+def to_markdown(res: dict, command: str,
+                title: str = "Fused decode kernels on MI355X: duration and HBM traffic per call",
+                note: str = "") -> str:
+    lines = [f"# {title}", "", "Commands (repo root, one MI355X):", "", "```", command.strip(),
+             "```", ""]
+    if note:
+        lines += [note.strip(), ""]
     if "FETCH_SIZE_scale" in res:
         lines.append(f"Calibration: a {res['copy_bytes'] / 2**20:.0f} MiB device copy reads "
                      f"FETCH_SIZE x {res['FETCH_SIZE_scale']:.3f} and WRITE_SIZE x "
@@ -379,6 +383,8 @@ def main(argv=None) -> int:
     ap.add_argument("--md")
     ap.add_argument("--json")
     ap.add_argument("--command", default="", help="command line recorded in the markdown")
+    ap.add_argument("--title", default=None, help="markdown title")
+    ap.add_argument("--note", default="", help="paragraph recorded under the commands")
     args = ap.parse_args(argv)
     manifest = json.loads(Path(args.manifest).read_text())
     res = summarize(manifest,
@@ -388,7 +394,8 @@ def main(argv=None) -> int:
                     raw=read_counters(args.raw) if args.raw else None)
     if args.json:
         Path(args.json).write_text(json.dumps(res, indent=1, sort_keys=True) + "\n")
-    text = to_markdown(res, args.command)
+    text = (to_markdown(res, args.command, args.title, args.note) if args.title
+            else to_markdown(res, args.command, note=args.note))
     if args.md:
         Path(args.md).write_text(text)
     print(text)

@@ -37,7 +37,8 @@ WARN makes the verdict INCOMPLETE.  The command exits non-zero on any FAIL
 or WARN.
 
     python -m decodebench_amd.validate --bench bench.json \\
-        --traffic profiles/traffic.json --output validation_report.md
+        --traffic profiles/traffic.json --kernel-trace profiles/kernel_trace_b1.json \\
+        --output validation_report.md
 """
 
 from __future__ import annotations
@@ -397,6 +398,10 @@ def main(argv=None) -> int:
     ap.add_argument("--bench", required=True, help="bench.py output (JSON line)")
     ap.add_argument("--traffic", required=True,
                     help="decodebench_amd.rocprof --json summary with the unfused rows")
+    ap.add_argument("--kernel-trace", default=None,
+                    help="decodebench_amd.rocprof --json summary of a --kernel-trace run; its "
+                         "per-call kernel time fills in workloads the traffic summary has no "
+                         "time for")
     ap.add_argument("--output", default="validation_report.md")
     ap.add_argument("--min-timing-samples", type=int, default=30)
     ap.add_argument("--f4-delta-tol", type=float, default=0.5)
@@ -410,6 +415,11 @@ def main(argv=None) -> int:
         ap.error("--min-timing-samples must be positive")
     bench = _load_json(args.bench)
     traffic = _load_json(args.traffic).get("workloads", {})
+    if args.kernel_trace:
+        for label, w in _load_json(args.kernel_trace).get("workloads", {}).items():
+            cell = traffic.setdefault(label, {})
+            if cell.get("call_us") is None and w.get("call_us") is not None:
+                cell["call_us"] = w["call_us"]
     checks, rep = validate(bench, traffic, args.min_timing_samples, args.f4_delta_tol,
                            args.allow_missing_counters, args.hypotheses)
     text = "\n".join(rep) + "\n"
