@@ -305,9 +305,22 @@ def summarize(manifest: dict, trace=None, fetch=None, write=None, raw=None) -> d
             calls = calls[warm[label]:]
             if calls:
                 per[label]["read_requests"] = per_call(calls)
+    # Traffic = reads + writes.  Reads come from the read requests counted by
+    # size when that run exists: the FETCH_SIZE factor is calibrated on
+    # 128-byte requests and doubles the 64-byte ones (kernel arguments, code,
+    # small records), which matters for calls of a few MB.
     for label, p in per.items():
-        if "fetch_bytes" in p and "write_bytes" in p:
-            p["traffic_bytes"] = p["fetch_bytes"] + p["write_bytes"]
+        if "write_bytes" not in p:
+            continue
+        if "fetch_bytes" in p:
+            p["traffic_fetch_scaled_bytes"] = p["fetch_bytes"] + p["write_bytes"]
+        if "read_requests" in p:
+            p["traffic_bytes"] = p["read_requests"]["bytes_by_size"] + p["write_bytes"]
+            p["traffic_source"] = "read requests by size + WRITE_SIZE"
+        elif "fetch_bytes" in p:
+            p["traffic_bytes"] = p["traffic_fetch_scaled_bytes"]
+            p["traffic_source"] = "FETCH_SIZE x calibration + WRITE_SIZE"
+        if "traffic_bytes" in p:
             p["traffic_over_algorithmic"] = p["traffic_bytes"] / p["algorithmic_bytes"]
     res["workloads"] = per
     return res
@@ -350,9 +363,17 @@ def to_markdown(res: dict, command: str,
                      "(kernel time summed over a call); their 'Algorithmic B' is the byte "
                      "model's total (`bytes_model.total_bytes` of the stage traces).")
         lines.append("")
+    by_size = any("read_requests" in p for p in res["workloads"].values())
+    if by_size:
+        lines.append("Traffic / algorithmic = (read bytes by request size + WRITE_SIZE) / "
+                     "algorithmic bytes. 'Fetch B' is FETCH_SIZE times the calibration factor, "
+                     "which is right for 128-byte requests and counts each 64-byte request "
+                     "(kernel arguments, code, small records) twice.")
+        lines.append("")
     lines += ["| Workload | Kernel us (median) | Call us | Algorithmic B | GB/s | % of 8 TB/s | "
-              "Fetch B | Write B | Traffic / algorithmic |",
-              "|---|---|---|---|---|---|---|---|---|"]
+              "Fetch B | " + ("Read B by size | " if by_size else "") +
+              "Write B | Traffic / algorithmic |",
+              "|---|---|---|---|---|---|---|---|---|" + ("---|" if by_size else "")]
     for label, p in res["workloads"].items():
         if p.get("kind") == "unfused":
             ku = f"{p.get('kernels_per_call', '?')} torch kernels (unfused stages)"
@@ -368,7 +389,11 @@ def to_markdown(res: dict, command: str,
         timing = (f"{ku} | {call:.2f} | {p['algorithmic_bytes']:,} | {gbs:.0f} | "
                   f"{gbs / 80:.1f}" if call is not None
                   else f" | | {p['algorithmic_bytes']:,} | | ")
-        lines.append(f"| {label} | {timing} | {num('fetch_bytes', ',.0f')} | "
+        rb = ""
+        if by_size:
+            rb = (f"{p['read_requests']['bytes_by_size']:,.0f}" if "read_requests" in p else "")
+            rb += " | "
+        lines.append(f"| {label} | {timing} | {num('fetch_bytes', ',.0f')} | {rb}"
                      f"{num('write_bytes', ',.0f')} | {num('traffic_over_algorithmic', '.3f')} |")
     return "\n".join(lines) + "\n"
 

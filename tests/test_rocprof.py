@@ -238,3 +238,34 @@ def test_raw_read_requests_by_size(tmp_path):
     g = res["workloads"]["gemv"]["read_requests"]
     assert g["bytes_by_size"] == 128 * 5 + 64 * 3 + 32 * 2
     assert g["fetch_size_formula_bytes"] == 128 * 3 + 64 * 5 + 32 * 2
+
+
+def test_traffic_uses_reads_by_size_when_the_raw_run_exists(tmp_path):
+    # 100 requests of 128 B and 20 of 64 B: 14,080 bytes read.  FETCH_SIZE's formula counts the
+    # 128-byte ones as 64 bytes (7,680 bytes = 7.5 KiB-units) and the copy calibrates x2, which
+    # doubles the 64-byte ones as well (15,360 bytes).
+    fetch = [(COPY, {"FETCH_SIZE": 512.0}), (PROBE, {"FETCH_SIZE": 512.0}),
+             (GEMV, {"FETCH_SIZE": 7.5})]
+    write = [(COPY, {"WRITE_SIZE": 1024.0}), (PROBE, {"WRITE_SIZE": 0.0}),
+             (GEMV, {"WRITE_SIZE": 0.5})]
+    one = {"TCC_EA0_RDREQ_sum": 8192, "TCC_EA0_RDREQ_32B_sum": 0, "TCC_BUBBLE_sum": 0,
+           "TCC_EA0_RDREQ_128B_sum": 8192}
+    gemv = {"TCC_EA0_RDREQ_sum": 120, "TCC_EA0_RDREQ_32B_sum": 0, "TCC_BUBBLE_sum": 0,
+            "TCC_EA0_RDREQ_128B_sum": 100}
+    for name, rows in (("f", fetch), ("w", write), ("r", [(COPY, one), (PROBE, one),
+                                                          (GEMV, gemv)])):
+        _counter_csv(tmp_path / f"{name}.csv", rows)
+    rd = lambda n: rocprof.read_counters(tmp_path / f"{n}.csv")  # noqa: E731
+    res = rocprof.summarize(READ_MANIFEST, fetch=rd("f"), write=rd("w"), raw=rd("r"))
+    g = res["workloads"]["gemv"]
+    assert g["fetch_bytes"] == pytest.approx(15360)
+    assert g["traffic_fetch_scaled_bytes"] == pytest.approx(15360 + 512)
+    assert g["traffic_bytes"] == pytest.approx(14080 + 512)
+    assert g["traffic_over_algorithmic"] == pytest.approx((14080 + 512) / 1000)
+    assert "by size" in g["traffic_source"]
+    md = rocprof.to_markdown(res, "cmd")
+    assert "Read B by size" in md and "14,080" in md
+    # without the raw run the scaled FETCH_SIZE is the read figure
+    res = rocprof.summarize(READ_MANIFEST, fetch=rd("f"), write=rd("w"))
+    assert res["workloads"]["gemv"]["traffic_bytes"] == pytest.approx(15360 + 512)
+    assert "FETCH_SIZE" in res["workloads"]["gemv"]["traffic_source"]
