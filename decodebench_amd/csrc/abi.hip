@@ -230,6 +230,10 @@ int check_f4(const char* fn, const void* q, const void* k, const void* v, const 
   if (!isfinite(scale)) return fail(DB_ERR_INVALID, "%s: scale must be finite", fn);
   if ((size_t)B * Hkv * L * D >= ((size_t)1 << 40))
     return fail(DB_ERR_INVALID, "%s: KV cache too large", fn);
+  // One (batch, kv-head) slice of K or V is addressed with 32-bit offsets.
+  if ((size_t)(L + 16) * D * 2 > (size_t)0x7fffffff)
+    return fail(DB_ERR_INVALID, "%s: KV length L=%d too long (at most %d)", fn, L,
+                0x7fffffff / (D * 2) - 16);
   return DB_OK;
 }
 
@@ -348,6 +352,10 @@ int db_tune(const char* key, int value) {
     if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8)
       return fail(DB_ERR_INVALID, "db_tune: f4_combine_groups must be 0, 1, 2, 4 or 8");
     t.f4_combine_groups = value;
+  } else if (!strcmp(key, "f4_depth")) {
+    if (value < 0 || value > 2)
+      return fail(DB_ERR_INVALID, "db_tune: f4_depth must be 0, 1 or 2");
+    t.f4_depth = value;
   } else if (!strcmp(key, "f4_min_tiles")) {
     if (value < 1) return fail(DB_ERR_INVALID, "db_tune: f4_min_tiles must be >= 1");
     t.f4_min_tiles = value;

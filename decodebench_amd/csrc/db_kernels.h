@@ -21,6 +21,7 @@ struct Tuning {
   int f4_merge = 0;            // 0: merge splits in a second launch; 1: same launch
   int f4_line = 0;             // F4 score layout: 0 auto, 1 whole-line K loads, 2 plain
   int f4_combine_groups = 0;   // split groups per F4 merge workgroup (0: auto)
+  int f4_depth = 0;            // F4 tiles in flight per wave: 0 auto, 1 or 2
 };
 Tuning& tuning();
 

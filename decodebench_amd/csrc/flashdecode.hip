@@ -12,8 +12,10 @@
 //  * Workgroups of one pair are numbered so that they all land on the same
 //    XCD (workgroup i is dispatched to XCD i % 8).
 //  * A wave walks 16-row tiles of its split (tile w, w + NW, ...) with two
-//    register sets of one tile each, so one or two tiles (8-16 KB) of K and
-//    V are in flight per wave.
+//    register sets of one tile each.  With DEPTH 2 one or two tiles (8-16
+//    KB) of K and V are in flight per wave; with DEPTH 1 a wave requests its
+//    next tile as soon as the oldest one has arrived and consumes the oldest
+//    while the next is in flight.
 //  * Scores for a tile come from four v_mfma_f32_16x16x32_f16: A = the
 //    K tile straight from HBM, B = Q^T with the G query heads as columns.
 //    The operands split each 128-byte line into its even and odd 16-byte
@@ -105,17 +107,22 @@ __device__ __forceinline__ float weight2(float m, float M) {
 // of another XCD's partials.  kSc1 is the sc1 cache-policy bit of a buffer
 // load.
 constexpr int kSc1 = 16;
+// s_waitcnt vmcnt(0) with the other counters left alone (gfx9 encoding).
+constexpr int kVmcnt0 = 0x0F70;
 __device__ __forceinline__ void store_coherent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int G, int NW, bool LINE>
+template <int G, int NW, bool LINE, int DEPTH>
 __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
   static_assert(G >= 1 && G <= 8, "query heads per KV head");
   constexpr int kThreads = NW * kWave;
 
-  __shared__ __align__(16) _Float16 s_v[NW][kTile][kVStride];  // per-wave V tile
-  __shared__ __align__(16) float s_o[NW][G][kD];  // per-wave outputs
+  // Per-wave V tile; after its last tile a wave leaves its G x D outputs in
+  // the same bytes for the workgroup merge.
+  __shared__ __align__(16) _Float16 s_v[NW][kTile][kVStride];
+  static_assert(sizeof(float) * G * kD <= sizeof(s_v[0]), "wave outputs fit a V tile");
+  auto s_o = [&](int w, int h) { return reinterpret_cast<float*>(&s_v[w][0][0]) + h * kD; };
   __shared__ float s_m[NW][G];
   __shared__ float s_l[NW][G];
 
@@ -193,6 +200,8 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
   const int t_end = min(a.ntiles, t_begin + a.tps);
   const int first = t_begin + wave;
   const int nt = first < t_end ? (t_end - first + NW - 1) / NW : 0;
+  // Global index of this wave's k-th tile.
+  auto tile_of = [&](int k) { return first + NW * k; };
   const int last_row = a.L - 1;
 
   // O^T accumulators: lane (g4, n16) holds O[head n16][16 b + 4 g4 + i].
@@ -309,21 +318,45 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
   // header.)  Measured on MI355X against sets of two tiles (two to four in
   // flight): 24.5 vs 25.0 us at batch 1, L = 32768, and 1-1.5% faster at
   // batch 4 and 8; deeper queues per wave only spread the tiles' arrival
-  // times and lengthen the tail of the slowest wave.
+  // times and lengthen the tail of the slowest wave.  DEPTH 1 (the batch-1
+  // whole-line kernel over long splits) waits for the oldest tile before
+  // requesting the next, so each wave keeps one tile in flight while it
+  // computes: at batch 1, L = 32768 (8 tiles per wave) 24.2 -> 24.0 us.
+  // Timestamps of an instrumented copy there show the waves of one
+  // workgroup finishing up to 4-6 us apart; handing tiles out from an LDS
+  // counter instead of the fixed w, w + NW, ... walk (so that faster waves
+  // take more) measured slower at every shape (0.2-0.9 us), as did
+  // interleaving the splits' tiles (split s taking tiles s, s + S, ...).
   if (nt > 0) {
     u4 ka[4], va[4], kb[4], vb[4];
-    load_tile(ka, va, first);
-    int k = 0;
-    for (; k + 3 <= nt; k += 2) {
-      load_tile(kb, vb, first + NW * (k + 1));
-      compute_tile(ka, va, first + NW * k);
-      load_tile(ka, va, first + NW * (k + 2));
-      compute_tile(kb, vb, first + NW * (k + 1));
+    load_tile(ka, va, tile_of(0));
+    if constexpr (DEPTH == 1) {
+      // One tile in flight: wait for the oldest tile, request the next one,
+      // then consume the oldest.
+      for (int k = 0; k < nt; k += 2) {
+        __builtin_amdgcn_s_waitcnt(kVmcnt0);
+        if (k + 1 < nt) load_tile(kb, vb, tile_of(k + 1));
+        __builtin_amdgcn_sched_barrier(0);
+        compute_tile(ka, va, tile_of(k));
+        if (k + 1 >= nt) break;
+        __builtin_amdgcn_s_waitcnt(kVmcnt0);
+        if (k + 2 < nt) load_tile(ka, va, tile_of(k + 2));
+        __builtin_amdgcn_sched_barrier(0);
+        compute_tile(kb, vb, tile_of(k + 1));
+      }
+    } else {
+      int k = 0;
+      for (; k + 3 <= nt; k += 2) {
+        load_tile(kb, vb, tile_of(k + 1));
+        compute_tile(ka, va, tile_of(k));
+        load_tile(ka, va, tile_of(k + 2));
+        compute_tile(kb, vb, tile_of(k + 1));
+      }
+      // One or two tiles remain; set A holds tile k.
+      if (k + 1 < nt) load_tile(kb, vb, tile_of(k + 1));
+      compute_tile(ka, va, tile_of(k));
+      if (k + 1 < nt) compute_tile(kb, vb, tile_of(k + 1));
     }
-    // One or two tiles remain; set A holds tile k.
-    if (k + 1 < nt) load_tile(kb, vb, first + NW * (k + 1));
-    compute_tile(ka, va, first + NW * k);
-    if (k + 1 < nt) compute_tile(kb, vb, first + NW * (k + 1));
   }
 
   // ---- merge the waves of the workgroup through LDS ---------------------
@@ -336,7 +369,7 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
   if (n16 < G) {
 #pragma unroll
     for (int b = 0; b < kD / 16; ++b)
-      *reinterpret_cast<f4*>(&s_o[wave][n16][16 * b + 4 * g4]) = o[b];
+      *reinterpret_cast<f4*>(s_o(wave, n16) + 16 * b + 4 * g4) = o[b];
   }
   __syncthreads();
 
@@ -353,7 +386,7 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
       const float e = weight2(s_m[w][h], M);
-      ow += e * s_o[w][h][d];
+      ow += e * s_o(w, h)[d];
       lw += e * s_l[w][h];
     }
     if (a.S == 1) {
@@ -547,26 +580,23 @@ __global__ __launch_bounds__(kGroups * 32) void f4_combine(F4Args a, int G) {
 
 using F4Fn = void (*)(F4Args);
 
-template <bool LINE>
-F4Fn pick_kernel_layout(int G, int waves) {
-  if (waves == 8) {
-    switch (G) {
-      case 1: return f4_kernel<1, 8, LINE>;
-      case 2: return f4_kernel<2, 8, LINE>;
-      case 4: return f4_kernel<4, 8, LINE>;
-      default: return f4_kernel<8, 8, LINE>;
-    }
-  }
+template <int NW, bool LINE, int DEPTH>
+F4Fn pick_heads(int G) {
   switch (G) {
-    case 1: return f4_kernel<1, 4, LINE>;
-    case 2: return f4_kernel<2, 4, LINE>;
-    case 4: return f4_kernel<4, 4, LINE>;
-    default: return f4_kernel<8, 4, LINE>;
+    case 1: return f4_kernel<1, NW, LINE, DEPTH>;
+    case 2: return f4_kernel<2, NW, LINE, DEPTH>;
+    case 4: return f4_kernel<4, NW, LINE, DEPTH>;
+    default: return f4_kernel<8, NW, LINE, DEPTH>;
   }
 }
 
-F4Fn pick_kernel(int G, int waves, bool line) {
-  return line ? pick_kernel_layout<true>(G, waves) : pick_kernel_layout<false>(G, waves);
+// One tile in flight (DEPTH 1) is built for the 8-wave whole-line kernel only.
+F4Fn pick_kernel(int G, int waves, bool line, int depth) {
+  if (waves == 8) {
+    if (line) return depth == 1 ? pick_heads<8, true, 1>(G) : pick_heads<8, true, 2>(G);
+    return pick_heads<8, false, 2>(G);
+  }
+  return line ? pick_heads<4, true, 2>(G) : pick_heads<4, false, 2>(G);
 }
 
 size_t round256(size_t n) { return (n + 255) / 256 * 256; }
@@ -640,8 +670,15 @@ hipError_t launch_f4(const void* q, const void* k, const void* v, void* o,
   const int tiles_per_wave = (a.tps + waves - 1) / waves;
   const bool line = tuning().f4_line == 1 ||
                     (tuning().f4_line == 0 && (tiles_per_wave <= 2 || pairs <= 8));
-  hipLaunchKernelGGL(pick_kernel(G, waves, line), dim3(pairs * a.S), dim3(waves * kWave), 0,
-                     stream, a);
+  // One tile in flight per wave for the whole-line kernel once its waves
+  // walk 4 or more tiles (measured on MI355X at batch 1, L = 32768: 24.2 ->
+  // 24.0 us); with 1-2 tiles per wave, and at L = 8192, both tiles are
+  // requested at once (one in flight was 0.3 us slower at L = 1024).
+  const int depth = tuning().f4_depth > 0
+                        ? tuning().f4_depth
+                        : (line && waves == 8 && tiles_per_wave >= 4 ? 1 : 2);
+  hipLaunchKernelGGL(pick_kernel(G, waves, line, depth), dim3(pairs * a.S),
+                     dim3(waves * kWave), 0, stream, a);
   if (a.S > 1 && !a.fused_merge) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

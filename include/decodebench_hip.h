@@ -200,8 +200,10 @@ int db_stream_read(const void* src, size_t bytes, int kb_per_wave, unsigned magi
  * "f4_waves" (4 or 8 waves per workgroup, 0: automatic), "f4_merge" (0: the
  * split merge runs in a second launch, the default; 1: in the same launch)
  * "f4_line" (F4 score-operand layout: 0 automatic, 1 whole-line K loads,
- * 2 16 keys x 64 bytes per load) and "f4_combine_groups" (split groups of
- * 32 threads per merge workgroup: 1, 2, 4 or 8; 0 automatic).
+ * 2 16 keys x 64 bytes per load), "f4_combine_groups" (split groups of
+ * 32 threads per merge workgroup: 1, 2, 4 or 8; 0 automatic) and "f4_depth"
+ * (tiles in flight per wave of the 8-wave whole-line F4 kernel: 1 or 2; 0
+ * automatic).
  * Process-wide; no counterpart in the reference. */
 int db_tune(const char* key, int value);
 

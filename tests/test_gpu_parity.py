@@ -424,6 +424,34 @@ def test_f4_score_layouts(B, Hq, Hkv, L, S):
     assert rel_l2(outs[0], outs[1]) < 2e-3
 
 
+# Shapes of the 8-wave whole-line kernel (at most 8 (batch, kv-head) pairs) run with one
+# and with two tiles in flight per wave (db_tune "f4_depth"): 8 tiles per wave (config 4,
+# L = 32768), 2, 3-4 with a partial last tile, 5-6, and 1-2 tiles.
+F4_DEPTH_CASES = [(1, 32, 8, 32768, None), (1, 32, 8, 8192, None), (1, 32, 8, 391, 1),
+                  (1, 32, 8, 720, 1), (1, 8, 8, 300, 3), (1, 16, 4, 5000, 2)]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,L,S", F4_DEPTH_CASES)
+def test_f4_tile_depths(B, Hq, Hkv, L, S):
+    """The two tile streams change when loads are issued, not what is
+    computed: the outputs are bit-identical and match the exact oracle."""
+    print(f"[f4-depth] B={B} Hq={Hq} Hkv={Hkv} L={L} S={S}", flush=True)
+    q, K, V = f4_inputs(B, Hq, Hkv, L, 3700 + B * 7 + L + (S or 0))
+    exact = cref.attention(q.numpy(), K.numpy(), V.numpy())
+    ref = stages.f4(q, K, V)
+    outs = []
+    try:
+        for depth in (1, 2):
+            ops.tune("f4_depth", depth)
+            o = ops.f4_flashdecode(q.cuda(), K.cuda(), V.cuda(), n_splits=S)
+            torch.cuda.synchronize()
+            assert_parity(o, ref, exact, F4_REL_L2, f"f4 depth {depth} B={B} L={L} S={S}")
+            outs.append(o.cpu())
+    finally:
+        ops.tune("f4_depth", 0)
+    assert torch.equal(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("L", [8192, 32768])
 def test_f4_full_batch_split_invariance(L):
     """B = 8 at full length: every split count gives the same answer, and
