@@ -143,8 +143,18 @@ hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
     hipError_t e = allow_large_lds(reinterpret_cast<const void*>(fn));
     if (e != hipSuccess) return e;
   }
-  const int waves = pick_waves(a.groups, cu_count);
   const int wv = fp8_long_rows ? kWavesFp8PlainLong : gemv_wg_waves(mode, w.fp8, nb);
+  // fp16 F1 with one row per wave: one 8-wave workgroup per CU, each wave
+  // walking its rows in turn, so every CU streams the same rows and runs the
+  // activation prologue once.  Measured on MI355X (graph back-to-back):
+  // F1-QKV 9.2 -> 9.05 us; with up to 32 waves per CU the 768 workgroups of
+  // 8 rows run in two rounds (two resident per CU at 91 VGPRs) and some CUs
+  // take a fourth.  The plain projection keeps the default (the fp16 decode
+  // layer measured 0.1-0.5 us slower with it).
+  const bool f1_persistent = mode == kGemvRmsNorm && !w.fp8 && nb == 1 && R == 1 &&
+                             wv == 8 && tuning().gemv_waves_per_cu <= 0;
+  const int waves = f1_persistent ? waves_for(a.groups, cu_count * wv)
+                                  : pick_waves(a.groups, cu_count);
   dim3 grid((waves + wv - 1) / wv, (B + nb - 1) / nb);
   hipLaunchKernelGGL(fn, grid, dim3(wv * kWave), lds, stream, a);
   return hipGetLastError();
