@@ -22,10 +22,8 @@
 //    stays in registers for the whole kernel in that B-operand layout;
 //    lane (g, n) holds x[b][k0 + 32 t + 8 g .. + 7] of its half.
 //  * Workgroup w owns groups w, w + grid, ...; each wave streams its slice of
-//    them with 16-byte loads.  When they fit in registers (up to 4 groups of
-//    one matrix or 2 of the gate/up pair) all are requested before the
-//    prologue; otherwise two register sets alternate (load set B, consume A,
-//    reload A, consume B).
+//    them with 16-byte loads through two register sets of one group each
+//    (load set B, consume A, reload A, consume B).
 //  * Each wave's partial sums (8 rows x 16 batch per group) go to LDS; after
 //    the last group the workgroup reduces the 8 K-slices and applies the
 //    epilogue (fp16 rounding, or SiLU(g) * u with the reference's rounding
@@ -424,31 +422,18 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
 
 using MfmaFn = void (*)(MfmaArgs);
 
-// ups > 0: one set of `ups` groups holds all of a workgroup's groups;
-// ups < 0: alternating sets of -ups groups.
+// One group per register set, two sets alternating (load set B, consume A,
+// reload A, consume B), so each wave has one or two groups of weights in
+// flight.  Measured on MI355X (graph back-to-back) against requesting all
+// of a workgroup's groups (up to 4) before the prologue, or sets of 2: F1-QKV
+// B = 4 10.95 -> 10.4 us, B = 8 11.45 -> 10.8-11.1 us, e4m3 B = 16 11.4 ->
+// 10.9 us, fp16 B = 16 14.7-14.8 -> 14.3-14.6 us.  The more weight requests
+// all CUs have outstanding while x (which every workgroup reads) is still
+// on its way, the later x arrives.
 template <int MODE, int KH, int BT, bool FP8>
 MfmaFn pick_ups(int ups) {
-  if constexpr (MODE == kGemvRmsNormSwiGLU && BT == 2) {
-    // The normalisation next to two batch tiles and a gate/up pair: one
-    // group pair per alternating set.
-    (void)ups;
-    return gemv_mfma_kernel<MODE, KH, BT, 1, false, FP8, false>;
-  } else if constexpr (gemv_is_swiglu(MODE)) {
-    return ups == 2 ? gemv_mfma_kernel<MODE, KH, BT, 2, true, FP8, false>
-                    : gemv_mfma_kernel<MODE, KH, BT, 1, false, FP8, false>;
-  } else if constexpr (MODE == kGemvRmsNorm && BT == 2) {
-    // Two batch tiles of F1 leave no registers for a whole-workgroup set
-    // next to the normalisation; always alternate two sets of 2 groups.
-    (void)ups;
-    return gemv_mfma_kernel<MODE, KH, BT, 2, false, FP8, false>;
-  } else {
-    switch (ups) {
-      case 2: return gemv_mfma_kernel<MODE, KH, BT, 2, true, FP8, false>;
-      case 3: return gemv_mfma_kernel<MODE, KH, BT, 3, true, FP8, false>;
-      case 4: return gemv_mfma_kernel<MODE, KH, BT, 4, true, FP8, false>;
-      default: return gemv_mfma_kernel<MODE, KH, BT, 2, false, FP8, false>;
-    }
-  }
+  (void)ups;
+  return gemv_mfma_kernel<MODE, KH, BT, 1, false, FP8, false>;
 }
 
 template <int MODE, int KH, bool FP8>
@@ -479,14 +464,6 @@ MfmaFn pick_mode(GemvMode mode, int kh, int bt, int ups, bool xb) {
     case kGemvRmsNormSwiGLU: return pick_kh<kGemvRmsNormSwiGLU, FP8>(kh, bt, ups);
     default: return pick_kh<kGemvPlain, FP8>(kh, bt, ups);
   }
-}
-
-// Register sets: everything at once when it fits (up to 4 groups of one
-// matrix, 2 of the gate/up pair, at 8 or 16 loads per group and matrix),
-// else alternating sets of 2 groups (1 for the pair).  See pick_ups.
-int pick_sets(GemvMode mode, int gpw) {
-  if (gemv_is_swiglu(mode)) return gpw <= 2 ? 2 : -1;
-  return gpw <= 2 ? 2 : (gpw <= 4 ? gpw : -2);
 }
 
 }  // namespace
@@ -529,7 +506,7 @@ hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
   const bool xb = nwm == 1 && B > kBatchTile && xb_bytes + part32 <= 152 * 1024;
   const int bt = xb || B >= 9 ? 2 : 1;  // batch column tiles held in registers
   const int pass = xb ? 32 : kBatchTile;
-  const int ups = pick_sets(mode, a.gpw);
+  const int ups = 1;
   const MfmaFn fn = w.fp8 ? pick_mode<true>(mode, kh, bt, ups, xb)
                           : pick_mode<false>(mode, kh, bt, ups, xb);
   const size_t lds = xb ? xb_bytes + part32
