@@ -7,7 +7,7 @@
 // batches from 3 rows (2 for the e4m3 gate/up pair) go to the MFMA kernel
 // (gemv_mfma.hip): the crossovers measured on MI355X at K = 4096.
 #include <mutex>
-#include <unordered_set>
+#include <unordered_map>
 
 #include "gemv_valu.h"
 
@@ -59,15 +59,24 @@ GemvFn gemv_pick_f1_two_rows(int u) {
 
 }  // namespace
 
-hipError_t allow_large_lds(const void* fn) {
+hipError_t allow_large_lds(const void* fn, size_t dynamic_bytes) {
   static std::mutex mu;
-  static std::unordered_set<const void*> done;
+  static std::unordered_map<const void*, size_t> limit;
   std::lock_guard<std::mutex> lock(mu);
-  if (done.count(fn)) return hipSuccess;
-  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     152 * 1024);
-  if (e == hipSuccess) done.insert(fn);
-  return e;
+  auto it = limit.find(fn);
+  if (it == limit.end()) {
+    // Whatever the 160 KB of LDS leave beside the kernel's static LDS, at
+    // most 152 KB.
+    hipFuncAttributes attr;
+    hipError_t e = hipFuncGetAttributes(&attr, fn);
+    if (e != hipSuccess) return e;
+    size_t cap = (size_t)160 * 1024 - attr.sharedSizeBytes;
+    if (cap > (size_t)152 * 1024) cap = (size_t)152 * 1024;
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)cap);
+    if (e != hipSuccess) return e;
+    it = limit.emplace(fn, cap).first;
+  }
+  return dynamic_bytes <= it->second ? hipSuccess : hipErrorInvalidValue;
 }
 
 hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
@@ -140,7 +149,7 @@ hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
                                     : gemv_pick_f16(mode, nb, U);
   const size_t lds = (size_t)nb * a.kp8 * 16;
   if (lds > 48 * 1024) {
-    hipError_t e = allow_large_lds(reinterpret_cast<const void*>(fn));
+    hipError_t e = allow_large_lds(reinterpret_cast<const void*>(fn), lds);
     if (e != hipSuccess) return e;
   }
   const int wv = fp8_long_rows ? kWavesFp8PlainLong : gemv_wg_waves(mode, w.fp8, nb);

@@ -121,38 +121,20 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   const int sbase =
       ((wave + (int)blockIdx.x + ((int)blockIdx.x >> 3)) & (kWavesM - 1)) * KH * 64;
   const int kcol = sbase + 32 * half + 8 * g4;  // fp16: this lane's column for k-step 0
+  // LDS slot of lane (g4, h, r8) at k-step t within a (batch tile, k-step)
+  // block of 64 activation chunks, where staged and XB activations live: the
+  // low four bits are XOR-swizzled by g4 and t so that both the staging
+  // writes (one row's 64 chunks: fixed r8, every t, h, g4) and the operand
+  // reads (64 consecutive lanes) spread over all LDS banks; unswizzled, the
+  // writes of one instruction met in 2 bank groups (a 32-way conflict).
+  auto xslot = [](int g, int h, int r, int t) {
+    return 16 * g + ((8 * h + r) ^ (g | ((t & 1) << 2)));
+  };
   // Column of this lane's activation chunk for k-step t.
   auto xcol = [&](int t) {
     if constexpr (FP8) return sbase + 128 * (t >> 1) + 64 * half + 16 * g4 + 8 * (t & 1);
     return kcol + 64 * t;
   };
-
-  // ---- activation slice -> registers (B operand), loads unconditional ----
-  // F1's gamma is shared by every batch row: thread t fetches 16-byte chunk t
-  // (K / 8 <= 512 chunks) for the LDS copy the normalisation reads.
-  u4 xr[BT][KH];
-#pragma unroll
-  for (int bt = 0; bt < BT; ++bt) {
-    const int xrow = b0 + min(8 * bt + r8, nb - 1);
-#pragma unroll
-    for (int t = 0; t < KH; ++t)
-      xr[bt][t] = ld16(a.x + (size_t)xrow * a.K + (FP8 ? xcol(t) : kcol + 64 * t));
-  }
-  // XB: rows 16..31 of the pass, in registers until they are written to LDS.
-  u4 xb[XB ? 2 : 1][KH];
-  if constexpr (XB) {
-#pragma unroll
-    for (int bt = 0; bt < 2; ++bt) {
-      const int xrow = b0 + min(16 + 8 * bt + r8, nb - 1);
-#pragma unroll
-      for (int t = 0; t < KH; ++t)
-        xb[bt][t] = ld16(a.x + (size_t)xrow * a.K + (FP8 ? xcol(t) : kcol + 64 * t));
-    }
-  }
-  u4 gchunk = {0, 0, 0, 0};
-  if constexpr (gemv_has_norm(MODE))
-    gchunk = ld16(a.gamma + 8 * min((int)threadIdx.x, a.K / 8 - 1));
-  __builtin_amdgcn_sched_barrier(0);
 
   // ---- the workgroup's groups: rows of group j are 8 (w + grid j) .. +7 --
   const int my_groups = min(a.gpw, (a.groups - (int)blockIdx.x + (int)gridDim.x - 1) /
@@ -178,42 +160,93 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
     }
   };
 
-  // x is read by every workgroup (B x K x 2 bytes per CU).  On MI355X its
-  // arrival, 1-2 us at batch 4 and 3-5 us at batch 16 with no weight
-  // traffic, stretches to 5-20 us when it queues behind the weights the
-  // other workgroups have requested.  With one batch tile the wave waits
-  // for its slice before requesting weights (batch 3-8 runs 0.4-1.3 us
-  // faster); with two tiles waiting costs more than it saves, and set A is
-  // requested first.
+  // ---- activation slice -> registers (B operand) ------------------------
+  // Two ways in.  Direct: each lane loads its own B operands; a load
+  // instruction then covers 8 batch rows x 128 bytes, 8 KB apart.  Staged:
+  // each wave loads its slice of every batch row contiguously -- lane l
+  // takes the slice's 16-byte chunk l, two rows per instruction when the
+  // slice is 32 chunks -- writes each chunk to the LDS slot of the lane and
+  // k-step that use it and reads its operands back.  Measured on MI355X:
+  // the direct pattern reads x (which all 256 workgroups read) 2.1x slower
+  // than contiguous rows for the same 16 KB per wave (4.6 vs 2.2 us per
+  // launch); staging makes one weight matrix at 9-32 rows 1.2-2.5 us
+  // faster (F1-QKV B = 16 14.5 -> 13.0 us, B = 32 21.7 -> 19.0 us, F1
+  // B = 16 12.6 -> 10.9 us, e4m3 F1-QKV B = 16 10.8 -> 9.7 us), while the
+  // gate/up pair at B = 16 (1.1 us) and every shape at 2-8 rows (0.4-0.7
+  // us) lose: there the weights, not x, set the pace, and the staging delays
+  // their first requests.  The staging area is the wave's XB tiles, or the
+  // partial-sum region, which nothing writes before the prologue's barrier.
+  constexpr bool kStage = BT == 2 && NWM == 1;
   const u4 zero4 = {0, 0, 0, 0};
+  u4 xr[BT][KH];
+  u4 xb[XB ? 2 : 1][KH];  // XB: rows 16..31 (norm modes: for their x^2 sums)
+  u4 gchunk = {0, 0, 0, 0};
+  // F1's gamma is shared by every batch row: thread t fetches 16-byte chunk t
+  // (K / 8 <= 512 chunks) for the LDS copy the normalisation reads.
+  auto load_gamma = [&]() {
+    if constexpr (gemv_has_norm(MODE))
+      gchunk = ld16(a.gamma + 8 * min((int)threadIdx.x, a.K / 8 - 1));
+  };
+  u4 wa[UPS][NWM][KW];
+  if constexpr (kStage) {
+    constexpr int kSliceChunks = 8 * KH;                // 16-byte chunks of a row's slice
+    constexpr int kRowsPerLoad = kWave / kSliceChunks;  // 1 (K = 4096) or 2 (K = 2048)
+    constexpr int kLoads = 8 * BT / kRowsPerLoad;       // per 8 BT rows
+    const int lchunk = lane % kSliceChunks;
+    const int lrow = lane / kSliceChunks;
+    // Consumer of chunk c: fp16 c = 8 t + 4 h + g4, e4m3 column order
+    // c = 16 (t >> 1) + 8 h + 2 g4 + (t & 1); lane 16 g4 + 8 h + r8.
+    const int ct = FP8 ? 2 * (lchunk >> 4) + (lchunk & 1) : lchunk >> 3;
+    const int ch = FP8 ? (lchunk >> 3) & 1 : (lchunk >> 2) & 1;
+    const int cg = FP8 ? (lchunk >> 1) & 3 : lchunk & 3;
+    u4* const stage =
+        (XB ? xbuf : reinterpret_cast<u4*>(part)) + (size_t)wave * BT * KH * kWave;
+    auto load_rows = [&](u4 (&dst)[kLoads], int r0) {
 #pragma unroll
-  for (int bt = 0; bt < BT; ++bt) {
-    const bool valid = 8 * bt + r8 < nb;
+      for (int i = 0; i < kLoads; ++i) {
+        const int rho = r0 + i * kRowsPerLoad + lrow;
+        dst[i] = ld16(a.x + (size_t)(b0 + min(rho, nb - 1)) * a.K + sbase + 8 * lchunk);
+      }
+    };
+    auto put_rows = [&](const u4 (&v)[kLoads], int r0) {
 #pragma unroll
-    for (int t = 0; t < KH; ++t) xr[bt][t] = valid ? xr[bt][t] : zero4;
-  }
-  if constexpr (XB) {
+      for (int i = 0; i < kLoads; ++i) {
+        const int rho = i * kRowsPerLoad + lrow;  // row within the 8 BT block
+        stage[((rho >> 3) * KH + ct) * kWave + xslot(cg, ch, rho & 7, ct)] =
+            r0 + rho < nb ? v[i] : zero4;
+      }
+    };
+    auto get_rows = [&](u4 (&dst)[BT][KH]) {
 #pragma unroll
-    for (int bt = 0; bt < 2; ++bt) {
-      const bool valid = 16 + 8 * bt + r8 < nb;
+      for (int bt = 0; bt < BT; ++bt)
 #pragma unroll
-      for (int t = 0; t < KH; ++t) xb[bt][t] = valid ? xb[bt][t] : zero4;
-    }
-  }
-  if constexpr (BT == 1) {
+        for (int t = 0; t < KH; ++t)
+          dst[bt][t] = stage[(bt * KH + t) * kWave + xslot(g4, half, r8, t)];
+    };
+    u4 xl[kLoads];
+    load_rows(xl, 0);
+    u4 xlb[XB ? kLoads : 1];
+    if constexpr (XB) load_rows(xlb, 16);
+    load_gamma();
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x and gamma are here
-  }
-  __builtin_amdgcn_sched_barrier(0);
-
-  if constexpr (XB) {
-    // Rows 16..31: their x^2 sums (norm modes), then raw into their LDS
-    // tiles before set A is requested, so both halves of the pass and set A
-    // are never live together.  Each wave writes and later reads back only
-    // its own slots (LDS keeps a wave's accesses in order).
+    put_rows(xl, 0);
+    get_rows(xr);
+    if constexpr (XB) {
+      // Rows 16..31 go to their LDS tiles, the same per-wave area, after
+      // rows 0..15 have been read back (a wave's LDS accesses complete in
+      // order).
+      put_rows(xlb, 16);
+      if constexpr (gemv_has_norm(MODE)) get_rows(xb);
+    }
+    // Without a normalisation barrier, one here keeps every wave's read-back
+    // ahead of the partial sums that later share the staging area.
+    if constexpr (!XB && !gemv_has_norm(MODE)) __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (XB && gemv_has_norm(MODE)) {
+      // Rows 16..31: their x^2 sums, from the copy read back from their LDS
+      // tiles (where they are normalised in place after the cross-wave sum).
 #pragma unroll
-    for (int bt = 0; bt < 2; ++bt) {
-      if constexpr (gemv_has_norm(MODE)) {
+      for (int bt = 0; bt < 2; ++bt) {
         float sb = 0.0f;
 #pragma unroll
         for (int t = 0; t < KH; ++t)
@@ -228,15 +261,37 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
         sb += __shfl_xor(sb, 32);
         if (lane < 8) red[wave][8 * (BT + bt) + lane] = sb;
       }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    load_set(wa, 0, true);  // every workgroup owns at least one group
+  } else {
 #pragma unroll
-      for (int t = 0; t < KH; ++t) xbuf[((wave * 2 + bt) * KH + t) * kWave + lane] = xb[bt][t];
+    for (int bt = 0; bt < BT; ++bt) {
+      const int xrow = b0 + min(8 * bt + r8, nb - 1);
+#pragma unroll
+      for (int t = 0; t < KH; ++t)
+        xr[bt][t] = ld16(a.x + (size_t)xrow * a.K + (FP8 ? xcol(t) : kcol + 64 * t));
+    }
+    load_gamma();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int bt = 0; bt < BT; ++bt) {
+      const bool valid = 8 * bt + r8 < nb;
+#pragma unroll
+      for (int t = 0; t < KH; ++t) xr[bt][t] = valid ? xr[bt][t] : zero4;
+    }
+    // With one batch tile the wave waits for its x slice before requesting
+    // weights (batch 3-8 ran 0.4-1.3 us faster); with two, set A goes out
+    // with x.
+    if constexpr (BT == 1) {
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x and gamma are here
     }
     __builtin_amdgcn_sched_barrier(0);
+    load_set(wa, 0, true);  // every workgroup owns at least one group
   }
-
-  u4 wa[UPS][NWM][KW];
-  load_set(wa, 0, true);  // every workgroup owns at least one group
   __builtin_amdgcn_sched_barrier(0);
+
 
   if constexpr (gemv_has_norm(MODE)) {
     // x^2 over this slice per batch row: in-lane, then over the two halves
@@ -271,7 +326,7 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
 #pragma unroll
         for (int t = 0; t < KH; ++t) {
           const u4 gv = s_gamma[(FP8 ? xcol(t) : kcol + 64 * t) / 8];
-          const u4 xv = xbuf[((wave * 2 + bt) * KH + t) * kWave + lane];
+          const u4 xv = xbuf[((wave * 2 + bt) * KH + t) * kWave + xslot(g4, half, r8, t)];
           u4 out;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
@@ -281,7 +336,7 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
             const float n1 = (float)to_h((float)xp[1] * inv);
             out[j] = pack_h2(n0 * (float)gp[0], n1 * (float)gp[1]);
           }
-          xbuf[((wave * 2 + bt) * KH + t) * kWave + lane] = out;
+          xbuf[((wave * 2 + bt) * KH + t) * kWave + xslot(g4, half, r8, t)] = out;
         }
       }
     }
@@ -351,7 +406,7 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
 #pragma unroll
             for (int t = 0; t < KH; ++t) {
               const u4 at = FP8 ? av[FP8 ? t : 0] : src[q][m][FP8 ? 0 : t];
-              const u4 bx = xbuf[((wave * 2 + bt) * KH + t) * kWave + lane];
+              const u4 bx = xbuf[((wave * 2 + bt) * KH + t) * kWave + xslot(g4, half, r8, t)];
               acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, at),
                                                            __builtin_bit_cast(h8, bx), acc, 0, 0,
                                                            0);
@@ -509,10 +564,15 @@ hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
   const int ups = 1;
   const MfmaFn fn = w.fp8 ? pick_mode<true>(mode, kh, bt, ups, xb)
                           : pick_mode<false>(mode, kh, bt, ups, xb);
-  const size_t lds = xb ? xb_bytes + part32
-                        : sizeof(float) * a.gpw * nwm * kWavesM * 8 * bt * kRowsPerGroup;
+  // The activation staging of one matrix at two batch tiles without XB (each
+  // wave's slice of the pass's rows, 16 bytes per lane per row tile and
+  // k-step) shares the partial-sum region.
+  const bool staged = bt == 2 && nwm == 1;
+  const size_t stage_bytes = staged ? (size_t)kWavesM * bt * kh * kWave * 16 : 0;
+  const size_t part16 = sizeof(float) * a.gpw * nwm * kWavesM * 8 * bt * kRowsPerGroup;
+  const size_t lds = xb ? xb_bytes + part32 : (part16 > stage_bytes ? part16 : stage_bytes);
   if (lds > 48 * 1024) {
-    hipError_t e = allow_large_lds(reinterpret_cast<const void*>(fn));
+    hipError_t e = allow_large_lds(reinterpret_cast<const void*>(fn), lds);
     if (e != hipSuccess) return e;
   }
   dim3 g(grid, (B + pass - 1) / pass);

@@ -81,9 +81,11 @@ GemvFn gemv_pick_fp8(GemvMode mode, int nb, int u);
 constexpr int kWavesFp8PlainLong = 8;
 GemvFn gemv_pick_fp8_plain_long(int u);
 
-// Raise a kernel's dynamic-LDS limit to 152 KB, once per kernel function
-// (the attribute is per function, not per launch).  Defined in gemv.hip.
-hipError_t allow_large_lds(const void* fn);
+// Raise a kernel's dynamic-LDS limit to what the 160 KB of LDS leave beside
+// its static LDS (at most 152 KB), once per kernel function (the attribute
+// is per function, not per launch), and check that `dynamic_bytes` fits.
+// Defined in gemv.hip.
+hipError_t allow_large_lds(const void* fn, size_t dynamic_bytes);
 
 // Rows per wave group, measured on MI355X at the decode shapes: fp16 keeps
 // 16 loads of 16 bytes per lane per tile (2 rows x 8 chunks, or the gate/up
