@@ -28,9 +28,10 @@
 //    the last group the workgroup reduces the 8 K-slices and applies the
 //    epilogue (fp16 rounding, or SiLU(g) * u with the reference's rounding
 //    points), storing only the final fp16 outputs.
-//  * Norm modes: each wave sums x^2 over its slice, the 8 partial sums meet in LDS,
-//    and every wave normalises its own x registers exactly as the torch stage
-//    rounds: fp16(fp16(x * inv_rms) * gamma), gamma read from an LDS copy.
+//  * Norm modes: each wave sums x^2 over its slice, the 8 partial sums meet
+//    in LDS, and every wave normalises its own x registers at the torch
+//    stage's rounding points, fp16(fp16(x * inv_rms) * gamma), gamma read
+//    from an LDS copy (see norm_mul).
 // Batches above 16 run as passes (grid.y), each reading the weights: one
 // weight matrix takes 32-row passes when the LDS holds rows 16..31 of x next
 // to the partial sums (XB), otherwise passes are 16 rows.
@@ -41,6 +42,26 @@ namespace dbk {
 namespace {
 
 constexpr int kWavesM = 8;
+
+// fp16(fp16(x * inv) * gamma) on 8 packed halves.  x * inv is one
+// v_fma_mix per half (f16 x f32 + 0, rounded to f16, written to the low or
+// high half of the result), the product with gamma one v_pk_mul_f16 per pair
+// (the exact fp16 x fp16 product rounded once, as the fp32 product the torch
+// stage rounds).  Three VALU operations per pair against seven through fp32
+// conversions.
+__device__ __forceinline__ u4 norm_mul(const u4& x, const u4& g, float inv) {
+  u4 out;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    unsigned r;
+    asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+        : "=&v"(r)
+        : "v"(x[j]), "v"(inv));
+    out[j] = __builtin_bit_cast(unsigned, as_h2(r) * as_h2(g[j]));
+  }
+  return out;
+}
 constexpr int kThreadsM = kWavesM * kWave;
 constexpr int kRowsPerGroup = 8;
 constexpr int kBatchTile = 16;
@@ -249,13 +270,7 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
       for (int bt = 0; bt < 2; ++bt) {
         float sb = 0.0f;
 #pragma unroll
-        for (int t = 0; t < KH; ++t)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const h2 p = as_h2(xb[bt][t][j]);
-            const float lo = (float)p[0], hi = (float)p[1];
-            sb += lo * lo + hi * hi;
-          }
+        for (int t = 0; t < KH; ++t) sb = dot8(xb[bt][t], xb[bt][t], sb);
         sb += __shfl_xor(sb, 8);
         sb += __shfl_xor(sb, 16);
         sb += __shfl_xor(sb, 32);
@@ -301,13 +316,7 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
     for (int bt = 0; bt < BT; ++bt) {
       ss[bt] = 0.0f;
 #pragma unroll
-      for (int t = 0; t < KH; ++t)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const h2 p = as_h2(xr[bt][t][j]);
-          const float lo = (float)p[0], hi = (float)p[1];
-          ss[bt] += lo * lo + hi * hi;
-        }
+      for (int t = 0; t < KH; ++t) ss[bt] = dot8(xr[bt][t], xr[bt][t], ss[bt]);
       ss[bt] += __shfl_xor(ss[bt], 8);
       ss[bt] += __shfl_xor(ss[bt], 16);
       ss[bt] += __shfl_xor(ss[bt], 32);
@@ -326,17 +335,8 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
 #pragma unroll
         for (int t = 0; t < KH; ++t) {
           const u4 gv = s_gamma[(FP8 ? xcol(t) : kcol + 64 * t) / 8];
-          const u4 xv = xbuf[((wave * 2 + bt) * KH + t) * kWave + xslot(g4, half, r8, t)];
-          u4 out;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const h2 xp = as_h2(xv[j]);
-            const h2 gp = as_h2(gv[j]);
-            const float n0 = (float)to_h((float)xp[0] * inv);
-            const float n1 = (float)to_h((float)xp[1] * inv);
-            out[j] = pack_h2(n0 * (float)gp[0], n1 * (float)gp[1]);
-          }
-          xbuf[((wave * 2 + bt) * KH + t) * kWave + xslot(g4, half, r8, t)] = out;
+          u4& xv = xbuf[((wave * 2 + bt) * KH + t) * kWave + xslot(g4, half, r8, t)];
+          xv = norm_mul(xv, gv, inv);
         }
       }
     }
@@ -347,19 +347,8 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
       for (int v = 0; v < kWavesM; ++v) tot += red[v][8 * bt + r8];
       const float inv = 1.0f / sqrtf(tot / (float)a.K + a.eps);
 #pragma unroll
-      for (int t = 0; t < KH; ++t) {
-        const u4 gv = s_gamma[(FP8 ? xcol(t) : kcol + 64 * t) / 8];
-        u4 out;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const h2 xp = as_h2(xr[bt][t][j]);
-          const h2 gp = as_h2(gv[j]);
-          const float n0 = (float)to_h((float)xp[0] * inv);
-          const float n1 = (float)to_h((float)xp[1] * inv);
-          out[j] = pack_h2(n0 * (float)gp[0], n1 * (float)gp[1]);
-        }
-        xr[bt][t] = out;
-      }
+      for (int t = 0; t < KH; ++t)
+        xr[bt][t] = norm_mul(xr[bt][t], s_gamma[(FP8 ? xcol(t) : kcol + 64 * t) / 8], inv);
     }
     // gamma shares the partial-sum region under XB: every wave must be done
     // with it before the first partial sum is stored.
