@@ -22,6 +22,9 @@ struct Tuning {
   int f4_line = 0;             // F4 score layout: 0 auto, 1 whole-line K loads, 2 plain
   int f4_combine_groups = 0;   // split groups per F4 merge workgroup (0: auto)
   int f4_depth = 0;            // F4 tiles in flight per wave: 0 auto, 1 or 2
+  int gemv_long_kc = 0;        // long-row MFMA GEMV k-steps per chunk: 0 auto, 2 or 4
+  int gemv_long_gpw = 0;       // long-row MFMA GEMV row groups per workgroup: 0 auto, 1, 2, 4
+  int gemv_long_stage = 0;     // long-row MFMA GEMV x: 0 auto, 1 direct, 2 LDS-staged
 };
 Tuning& tuning();
 
@@ -65,7 +68,7 @@ hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
 
 // MFMA variant for batches of up to 16 rows per pass (gemv_mfma.hip), fp16
 // or e4m3 weights, K in {2048, 4096}.
-bool gemv_mfma_supported(int B, int K, int N);
+bool gemv_mfma_supported(GemvMode mode, int B, int K, int N);
 hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
                             const GemvWeights& w, void* y, int B, int K, int N, float eps,
                             int cu_count, hipStream_t stream);

@@ -88,7 +88,7 @@ hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
   // would run two 2-row passes, 1.5-1.8x the MFMA time.
   const int auto_min = gemv_is_swiglu(mode) && w.fp8 ? 2 : 3;
   const int mfma_min = forced_min > 0 ? forced_min : auto_min;
-  if (B >= mfma_min && gemv_mfma_supported(B, K, N))
+  if (B >= mfma_min && gemv_mfma_supported(mode, B, K, N))
     return launch_gemv_mfma(mode, x, gamma, w, y, B, K, N, eps, cu_count, stream);
   GemvArgs a;
   a.x = static_cast<const _Float16*>(x);

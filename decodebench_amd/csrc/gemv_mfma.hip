@@ -36,6 +36,8 @@
 // Batches above 16 run as passes (grid.y), each reading the weights: one
 // weight matrix takes 32-row passes when the LDS holds rows 16..31 of x next
 // to the partial sums (XB), otherwise passes are 16 rows.
+// Plain GEMV with longer rows (K a multiple of 2048 above 4096, the down
+// projection) takes gemv_mfma_long_kernel, which streams x as well.
 #include "gemv_valu.h"
 
 namespace dbk {
@@ -65,6 +67,15 @@ __device__ __forceinline__ u4 norm_mul(const u4& x, const u4& g, float inv) {
     out[j] = __builtin_bit_cast(unsigned, as_h2(r) * as_h2(g[j]));
   }
   return out;
+}
+// LDS slot of lane (g4, h, r8) at k-step t within a (batch tile, k-step)
+// block of 64 activation chunks, where staged and XB activations live: the
+// low four bits are XOR-swizzled by g4 and t so that both the staging
+// writes (one row's chunks: fixed r8, every t, h, g4) and the operand reads
+// (64 consecutive lanes) spread over all LDS banks; unswizzled, the writes
+// of one instruction met in 2 bank groups (a 32-way conflict).
+__device__ __forceinline__ int xslot(int g, int h, int r, int t) {
+  return 16 * g + ((8 * h + r) ^ (g | ((t & 1) << 2)));
 }
 constexpr int kThreadsM = kWavesM * kWave;
 constexpr int kRowsPerGroup = 8;
@@ -146,15 +157,6 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   const int sbase =
       ((wave + (int)blockIdx.x + ((int)blockIdx.x >> 3)) & (kWavesM - 1)) * KH * 64;
   const int kcol = sbase + 32 * half + 8 * g4;  // fp16: this lane's column for k-step 0
-  // LDS slot of lane (g4, h, r8) at k-step t within a (batch tile, k-step)
-  // block of 64 activation chunks, where staged and XB activations live: the
-  // low four bits are XOR-swizzled by g4 and t so that both the staging
-  // writes (one row's 64 chunks: fixed r8, every t, h, g4) and the operand
-  // reads (64 consecutive lanes) spread over all LDS banks; unswizzled, the
-  // writes of one instruction met in 2 bank groups (a 32-way conflict).
-  auto xslot = [](int g, int h, int r, int t) {
-    return 16 * g + ((8 * h + r) ^ (g | ((t & 1) << 2)));
-  };
   // Column of this lane's activation chunk for k-step t.
   auto xcol = [&](int t) {
     if constexpr (FP8) return sbase + 128 * (t >> 1) + 64 * half + 16 * g4 + 8 * (t & 1);
@@ -468,6 +470,206 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   }
 }
 
+// ---- long rows: K a multiple of 2048 above 4096 ---------------------------
+// At K = 14336 (the down projection) a 16-row activation slice would take
+// 224 VGPRs, so here both operands stream.  Wave v of workgroup w owns the
+// same XCD-staggered K / 8 slice as above and walks it in chunks of KC
+// k-steps (64 KC columns, dealt out over the halves and lane groups as
+// above).  Per chunk it loads the pass's BT batch tiles of x and the chunk
+// of each of the workgroup's GPW groups, and the MFMA sums accumulate in
+// registers across chunks; two register sets alternate (load chunk c + 1,
+// consume chunk c).  Batch rows past the batch read x's last row and rows
+// past N read W's last row: batch column n of an MFMA sees only x row n and
+// output row m only weight row m, and those columns and rows are never
+// stored.  Plain GEMV only: a norm would need all of x before the first
+// product.
+// XS: x is loaded contiguously -- lane l takes 16-byte piece l % 8 KC of
+// the chunk of batch row l / 8 KC, 64 / (8 KC) rows per instruction -- and
+// staged through the wave's LDS tile (the xslot layout) into B operands;
+// otherwise each lane loads its own B operands (8 batch rows x 128 bytes
+// per instruction).
+template <int KC, int BT, int GPW, bool FP8, bool XS>
+__global__ __launch_bounds__(kThreadsM) void gemv_mfma_long_kernel(MfmaArgs a) {
+  constexpr int KWC = FP8 ? KC / 2 : KC;  // 16-byte weight loads per row and chunk
+  constexpr int kPass = 8 * BT;
+  constexpr int kXL = BT * KC;            // x loads per chunk, either way
+  static_assert(!FP8 || KC % 2 == 0, "an e4m3 load spans two k-steps");
+  // [group][wave][batch][row quad]: rows 4 i .. 4 i + 3 of a group
+  __shared__ f4 part[GPW][kWavesM][kPass][2];
+  // XS: each wave's x tile, [batch tile][k-step][slot] (BT KC KB per wave)
+  extern __shared__ __align__(16) unsigned char dyn_lds[];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int c16 = lane & 15;
+  const int g4 = lane >> 4;
+  const int r8 = c16 & 7;
+  const int half = c16 >> 3;
+  const int bx = blockIdx.x;
+  const int b0 = blockIdx.y * kPass;
+  const int nb = min(kPass, a.B - b0);
+  const int slice = a.K / kWavesM;
+  const int nch = slice / (64 * KC);
+  const int sbase = ((wave + bx + (bx >> 3)) & (kWavesM - 1)) * slice;
+  // This lane's first column: fp16 k-step t of chunk c covers
+  // 64 (KC c + t) + 32 h + 8 g4; e4m3 load p covers 64 KC c + 128 p + 64 h
+  // + 16 g4 (k-steps 2p and 2p + 1, x 8 columns apart).
+  const int lcol = sbase + (FP8 ? 64 * half + 16 * g4 : 32 * half + 8 * g4);
+  const int my_groups = min(GPW, (a.groups - bx + (int)gridDim.x - 1) / (int)gridDim.x);
+
+  // x.  Direct: a pointer per batch tile.  Staged: load i covers rows
+  // rho = i R + l / (8 KC) (R = 64 / (8 KC) rows per instruction), at a
+  // 32-bit byte offset from the pass's first row (so the loads take the
+  // scalar-base form); rows past the batch read its last row.  Its piece goes
+  // to LDS slot ((rho >> 3) KC + ct) 64 + xslot(cg, ch, rho & 7, ct), where
+  // rho & 7 = (i R & 7) | l / (8 KC) carries nothing into the bits xslot's
+  // swizzle touches: the slot is put_base[(i R & 7) / R] plus a constant.
+  constexpr int kPieces = 8 * KC;
+  constexpr int kRowsPerLd = kWave / kPieces;
+  constexpr int kPutVariants = 8 / kRowsPerLd;
+  const _Float16* xp[XS ? 1 : BT];
+  unsigned xoff_b[XS ? kXL : 1];
+  int put_base[XS ? kPutVariants : 1];
+  int get_base[2];
+  if constexpr (XS) {
+    const int piece = lane % kPieces;
+    const int lrow = lane / kPieces;
+    // consumer of piece cc: fp16 cc = 8 t + 4 h + g4, e4m3 cc = 16 (t >> 1)
+    // + 8 h + 2 g4 + (t & 1)
+    const int ct = FP8 ? 2 * (piece >> 4) + (piece & 1) : piece >> 3;
+    const int ch = FP8 ? (piece >> 3) & 1 : (piece >> 2) & 1;
+    const int cg = FP8 ? (piece >> 1) & 3 : piece & 3;
+    xp[0] = a.x + (size_t)b0 * a.K + sbase;
+#pragma unroll
+    for (int i = 0; i < kXL; ++i)
+      xoff_b[i] = 2u * ((unsigned)min(i * kRowsPerLd + lrow, nb - 1) * (unsigned)a.K +
+                        8u * (unsigned)piece);
+    const int sw = cg | ((ct & 1) << 2);
+#pragma unroll
+    for (int v = 0; v < kPutVariants; ++v)
+      put_base[v] = ct * kWave + 16 * cg + (((8 * ch) | lrow) ^ sw ^ (v * kRowsPerLd));
+#pragma unroll
+    for (int p = 0; p < 2; ++p) get_base[p] = xslot(g4, half, r8, p);
+  } else {
+#pragma unroll
+    for (int bt = 0; bt < BT; ++bt)
+      xp[bt] = a.x + (size_t)(b0 + min(8 * bt + r8, nb - 1)) * a.K + lcol;
+  }
+  u4* const tile = reinterpret_cast<u4*>(dyn_lds) + (size_t)wave * kXL * kWave;
+  const unsigned char* wp[GPW];
+  const int esz = FP8 ? 1 : 2;
+#pragma unroll
+  for (int q = 0; q < GPW; ++q) {
+    const int grp = bx + (int)gridDim.x * min(q, my_groups - 1);
+    const int row = min(grp * kRowsPerGroup + r8, a.N - 1);
+    wp[q] = static_cast<const unsigned char*>(a.w0) + ((size_t)row * a.K + lcol) * esz;
+  }
+  auto xoff = [](int t) { return FP8 ? 128 * (t >> 1) + 8 * (t & 1) : 64 * t; };
+
+  auto load = [&](u4 (&xs)[kXL], u4 (&ws)[GPW][KWC], int c) {
+    const int c0 = 64 * KC * c;
+#pragma unroll
+    for (int q = 0; q < GPW; ++q)
+#pragma unroll
+      for (int p = 0; p < KWC; ++p)
+        ws[q][p] = ld_stream(wp[q] + (size_t)(c0 + 64 * p * (FP8 ? 2 : 1)) * esz);
+    if constexpr (XS) {
+      const unsigned char* xc = reinterpret_cast<const unsigned char*>(xp[0] + c0);
+#pragma unroll
+      for (int i = 0; i < kXL; ++i) xs[i] = ld16(xc + xoff_b[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kXL; ++i) xs[i] = ld16(xp[i / KC] + c0 + xoff(i % KC));
+    }
+  };
+  f4 acc[GPW][BT];
+#pragma unroll
+  for (int q = 0; q < GPW; ++q)
+#pragma unroll
+    for (int bt = 0; bt < BT; ++bt) acc[q][bt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  auto consume = [&](const u4 (&xl)[kXL], const u4 (&ws)[GPW][KWC]) {
+    u4 xs[kXL];
+    if constexpr (XS) {
+      // A wave's LDS accesses complete in order: the previous chunk's reads
+      // are done before these writes land.
+#pragma unroll
+      for (int i = 0; i < kXL; ++i)
+        tile[((i * kRowsPerLd) >> 3) * KC * kWave + put_base[((i * kRowsPerLd) & 7) / kRowsPerLd]] =
+            xl[i];
+#pragma unroll
+      for (int bt = 0; bt < BT; ++bt)
+#pragma unroll
+        for (int t = 0; t < KC; ++t)
+          xs[bt * KC + t] = tile[(bt * KC + t) * kWave + get_base[t & 1]];
+    } else {
+#pragma unroll
+      for (int i = 0; i < kXL; ++i) xs[i] = xl[i];
+    }
+    u4 av[GPW][KC];
+#pragma unroll
+    for (int q = 0; q < GPW; ++q) {
+      if constexpr (FP8) {
+#pragma unroll
+        for (int p = 0; p < KWC; ++p) e4m3x16_to_h(ws[q][p], av[q][2 * p], av[q][2 * p + 1]);
+      } else {
+#pragma unroll
+        for (int t = 0; t < KC; ++t) av[q][t] = ws[q][t];
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < KC; ++t)
+#pragma unroll
+      for (int q = 0; q < GPW; ++q)
+#pragma unroll
+        for (int bt = 0; bt < BT; ++bt)
+          acc[q][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              __builtin_bit_cast(h8, av[q][t]), __builtin_bit_cast(h8, xs[bt * KC + t]),
+              acc[q][bt], 0, 0, 0);
+  };
+
+  u4 xa[kXL], wa[GPW][KWC], xb[kXL], wb[GPW][KWC];
+  load(xa, wa, 0);
+  int c = 0;
+  for (; c + 3 <= nch; c += 2) {
+    load(xb, wb, c + 1);
+    consume(xa, wa);
+    load(xa, wa, c + 2);
+    consume(xb, wb);
+  }
+  // One or two chunks remain; set A holds the first.
+  if (c + 1 < nch) load(xb, wb, c + 1);
+  consume(xa, wa);
+  if (c + 1 < nch) consume(xb, wb);
+
+  // D[4 g4 + i][c16]: rows 0..7 x batch 0..7 (half 0) in lanes (g4 < 2,
+  // c16 < 8), their half-1 partners 40 lanes higher.
+#pragma unroll
+  for (int q = 0; q < GPW; ++q)
+#pragma unroll
+    for (int bt = 0; bt < BT; ++bt) {
+      f4 v = acc[q][bt];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] += __shfl(v[i], lane + 40);
+      if (g4 < 2 && c16 < 8) part[q][wave][8 * bt + c16][g4] = v;
+    }
+  __syncthreads();
+
+  // ---- reduce the 8 K-slices, row scales, fp16 store ---------------------
+  const float* pf = reinterpret_cast<const float*>(&part[0][0][0][0]);
+  for (int idx = threadIdx.x; idx < my_groups * kPass * kRowsPerGroup; idx += kThreadsM) {
+    const int q = idx / (kPass * kRowsPerGroup);
+    const int n = (idx / kRowsPerGroup) % kPass;
+    const int r = idx % kRowsPerGroup;
+    const int row = (bx + (int)gridDim.x * q) * kRowsPerGroup + r;
+    if (n >= nb || row >= a.N) continue;
+    float s = 0.0f;
+#pragma unroll
+    for (int v = 0; v < kWavesM; ++v) s += pf[((q * kWavesM + v) * kPass + n) * kRowsPerGroup + r];
+    if constexpr (FP8) s *= a.s0[row];
+    a.y[(size_t)(b0 + n) * a.N + row] = to_h(s);
+  }
+}
+
 using MfmaFn = void (*)(MfmaArgs);
 
 // One group per register set, two sets alternating (load set B, consume A,
@@ -514,13 +716,85 @@ MfmaFn pick_mode(GemvMode mode, int kh, int bt, int ups, bool xb) {
   }
 }
 
+
+// Four groups of 32 batch rows in 4-k-step chunks would spill (256 VGPRs
+// and scratch); that combination takes 2-k-step chunks.
+template <int KC, int BT, bool FP8, bool XS>
+MfmaFn pick_long_gpw(int gpw) {
+  constexpr int KC4 = KC == 4 && BT == 4 ? 2 : KC;
+  return gpw == 1 ? gemv_mfma_long_kernel<KC, BT, 1, FP8, XS>
+                  : gpw == 2 ? gemv_mfma_long_kernel<KC, BT, 2, FP8, XS>
+                             : gemv_mfma_long_kernel<KC4, BT, 4, FP8, XS>;
+}
+
+template <int KC, bool FP8, bool XS>
+MfmaFn pick_long_bt(int bt, int gpw) {
+  return bt == 1 ? pick_long_gpw<KC, 1, FP8, XS>(gpw)
+                 : bt == 2 ? pick_long_gpw<KC, 2, FP8, XS>(gpw)
+                           : pick_long_gpw<KC, 4, FP8, XS>(gpw);
+}
+
+template <bool FP8, bool XS>
+MfmaFn pick_long_kc(int kc, int bt, int gpw) {
+  return kc == 2 ? pick_long_bt<2, FP8, XS>(bt, gpw) : pick_long_bt<4, FP8, XS>(bt, gpw);
+}
+
+template <bool FP8>
+MfmaFn pick_long(int kc, int bt, int gpw, bool xs) {
+  return xs ? pick_long_kc<FP8, true>(kc, bt, gpw) : pick_long_kc<FP8, false>(kc, bt, gpw);
+}
+
 }  // namespace
 
-bool gemv_mfma_supported(int B, int K, int N) {
+// Long rows (plain GEMV, K a multiple of 2048 above 4096): both operands
+// stream in K chunks.
+static bool long_rows(GemvMode mode, int K) {
+  return mode == kGemvPlain && K > 4096 && K % 2048 == 0;
+}
+
+bool gemv_mfma_supported(GemvMode mode, int B, int K, int N) {
   if (B < 2 || N < 1) return false;
+  if (long_rows(mode, K)) return true;
   if (K != 2048 && K != 4096) return false;  // K / 512 = 4 or 8 k-steps per half
   const int groups = (N + kRowsPerGroup - 1) / kRowsPerGroup;
   return groups <= 256 * kMaxGroupsPerWg;
+}
+
+static hipError_t launch_gemv_mfma_long(const MfmaArgs& a0, bool fp8, int cu_count,
+                                        hipStream_t stream) {
+  MfmaArgs a = a0;
+  // Batch tiles of 8 per pass: up to 32 rows in one pass, so the weights
+  // are read once up to batch 32.
+  const int bt = a.B <= 8 ? 1 : a.B <= 16 ? 2 : 4;
+  // Chunk size, measured at [4096, 14336] (µs, staged x, 2 groups per
+  // workgroup, 4- against 2-k-step chunks): e4m3 at 3-8 rows 11.9 / 13.4
+  // against 13.3 / 14.2 (its 2-k-step sets hold only 2 KB of weights per
+  // wave); fp16 at 8 rows 21.5 against 21.1, at 16 rows 25.3 against 24.8;
+  // at 32 rows the 4-k-step sets spill.
+  int kc = tuning().gemv_long_kc;
+  if (kc == 0) kc = fp8 && bt == 1 ? 4 : 2;
+  int gpw = tuning().gemv_long_gpw;
+  if (gpw == 0) {
+    gpw = 4;
+    for (int g = 1; g < 4; g *= 2)
+      if ((a.groups + g - 1) / g <= cu_count) {
+        gpw = g;
+        break;
+      }
+  }
+  a.gpw = gpw;
+  const int grid = (a.groups + gpw - 1) / gpw;
+  if (bt == 4 && gpw == 4) kc = 2;
+  const bool xs = tuning().gemv_long_stage != 1;
+  const MfmaFn fn = fp8 ? pick_long<true>(kc, bt, gpw, xs) : pick_long<false>(kc, bt, gpw, xs);
+  const size_t lds = xs ? (size_t)kWavesM * bt * kc * kWave * 16 : 0;
+  if (lds > 48 * 1024) {
+    hipError_t e = allow_large_lds(reinterpret_cast<const void*>(fn), lds);
+    if (e != hipSuccess) return e;
+  }
+  dim3 g(grid, (a.B + 8 * bt - 1) / (8 * bt));
+  hipLaunchKernelGGL(fn, g, dim3(kThreadsM), lds, stream, a);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
@@ -539,6 +813,7 @@ hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
   a.N = N;
   a.eps = eps;
   a.groups = (N + kRowsPerGroup - 1) / kRowsPerGroup;
+  if (long_rows(mode, K)) return launch_gemv_mfma_long(a, w.fp8, cu_count, stream);
   int grid = min(a.groups, cu_count);
   a.gpw = (a.groups + grid - 1) / grid;
   if (a.gpw > kMaxGroupsPerWg) a.gpw = kMaxGroupsPerWg;

@@ -201,9 +201,13 @@ int db_stream_read(const void* src, size_t bytes, int kb_per_wave, unsigned magi
  * split merge runs in a second launch, the default; 1: in the same launch)
  * "f4_line" (F4 score-operand layout: 0 automatic, 1 whole-line K loads,
  * 2 16 keys x 64 bytes per load), "f4_combine_groups" (split groups of
- * 32 threads per merge workgroup: 1, 2, 4 or 8; 0 automatic) and "f4_depth"
+ * 32 threads per merge workgroup: 1, 2, 4 or 8; 0 automatic), "f4_depth"
  * (tiles in flight per wave of the 8-wave whole-line F4 kernel: 1 or 2; 0
- * automatic).
+ * automatic), "gemv_long_kc" (k-steps of 32 columns per chunk of the
+ * long-row MFMA GEMV: 2 or 4; 0 automatic), "gemv_long_gpw" (its 8-row
+ * groups per workgroup: 1, 2 or 4; 0 automatic) and "gemv_long_stage" (its
+ * activations: 1 loaded as B operands, 2 staged through LDS; 0 automatic,
+ * staged).
  * Process-wide; no counterpart in the reference. */
 int db_tune(const char* key, int value);
 

@@ -171,6 +171,12 @@ def test_tune_keys(lib):
     assert lib.db_tune(b"f4_depth", 3) == -1
     assert lib.db_tune(b"f4_depth", 0) == 0
     assert lib.db_tune(b"f4_waves", 16) == -1
+    assert lib.db_tune(b"gemv_long_kc", 3) == -1
+    assert lib.db_tune(b"gemv_long_gpw", 3) == -1
+    assert lib.db_tune(b"gemv_long_kc", 0) == 0
+    assert lib.db_tune(b"gemv_long_gpw", 0) == 0
+    assert lib.db_tune(b"gemv_long_stage", 3) == -1
+    assert lib.db_tune(b"gemv_long_stage", 0) == 0
     assert lib.db_tune(b"f4_merge", 0) == 0
     assert lib.db_tune(b"f4_blocks_per_cu", 2) == 0
     assert lib.db_tune(b"f4_blocks_per_cu", 1) == 0   # back to the default

@@ -195,6 +195,75 @@ def test_mfma_and_valu_gemv_paths_agree():
         assert rel_l2(a.float().cpu().numpy(), b.float().cpu().numpy()) < 1e-3
 
 
+# --------------------------------------------------- long rows (MFMA, streamed x)
+# Plain GEMV with K a multiple of 2048 above 4096 -- the decode chain's down
+# projection, K = 14336 -- streams both operands in K chunks: batch tiles of
+# 8, 16 and 32 rows in one pass, two passes above 32, N not a multiple of
+# the 8-row group, fewer groups than CUs, fp16 and e4m3 weights.
+LONG_CASES = [
+    ("f16", 3, 14336, 4096), ("f16", 16, 14336, 4096), ("f16", 32, 14336, 1000),
+    ("f16", 9, 8192, 4100), ("f16", 40, 6144, 520), ("f16", 12, 14336, 7),
+    ("fp8", 8, 14336, 4096), ("fp8", 32, 14336, 2048), ("fp8", 17, 28672, 300),
+    ("fp8", 5, 6144, 9), ("fp8", 33, 10240, 264),
+]
+
+
+@pytest.mark.parametrize("dtype,B,K,N", LONG_CASES)
+def test_long_row_gemv_mfma_parity(dtype, B, K, N):
+    from decodebench_amd.quant import quantize_e4m3_rows
+
+    print(f"[long] {dtype} B={B} K={K} N={N}", flush=True)
+    gen = torch.Generator().manual_seed(8000 + B + K + N)
+    x = randn(gen, (B, K))
+    W = randn(gen, (N, K), std=1.0 / math.sqrt(K))
+    if dtype == "fp8":
+        Wq, s = quantize_e4m3_rows(W)
+        y = ops.gemv(x.cuda(), Wq.cuda(), w_scale=s.cuda())
+        ref = stages.gemv_fp8(x, Wq, s)
+        exact = cref.gemv_fp8_exact(x.numpy(), Wq.view(torch.uint8).numpy(), s.numpy())
+    else:
+        y = ops.gemv(x.cuda(), W.cuda())
+        ref, exact = stages.gemv(x, W), cref.gemv_exact(x.numpy(), W.numpy())
+    torch.cuda.synchronize()
+    assert y.shape == (B, N)
+    assert_parity(y, ref, exact, F12_REL_L2, f"long {dtype} B={B} K={K} N={N}")
+
+
+def test_long_row_gemv_launch_shapes_agree():
+    """The down-projection shape at 2, 16 and 32 rows through both activation
+    paths (direct and LDS-staged), every chunk size and row-group count of the
+    long-row kernel, and through the VALU kernel, agrees to fp32 summation
+    order."""
+    from decodebench_amd.quant import quantize_e4m3_rows
+
+    gen = torch.Generator().manual_seed(79)
+    lib = ops.load_library()
+    W = randn(gen, (4096, 14336), std=1.0 / math.sqrt(14336))
+    Wq, s = (t.cuda() for t in quantize_e4m3_rows(W))
+    W = W.cuda()
+    try:
+        for B in (2, 16, 32):
+            x = randn(gen, (B, 14336)).cuda()
+            assert lib.db_tune(b"gemv_mfma_min_batch", 1 << 20) == 0
+            base = (ops.gemv(x, W), ops.gemv(x, Wq, w_scale=s))
+            assert lib.db_tune(b"gemv_mfma_min_batch", 2) == 0
+            for stage in (1, 2):
+                for kc in (2, 4):
+                    for gpw in (1, 2, 4):
+                        assert lib.db_tune(b"gemv_long_stage", stage) == 0
+                        assert lib.db_tune(b"gemv_long_kc", kc) == 0
+                        assert lib.db_tune(b"gemv_long_gpw", gpw) == 0
+                        got = (ops.gemv(x, W), ops.gemv(x, Wq, w_scale=s))
+                        for a, b in zip(got, base):
+                            err = rel_l2(a.float().cpu().numpy(), b.float().cpu().numpy())
+                            assert err < 1e-3, \
+                                f"B={B} stage={stage} kc={kc} gpw={gpw}: rel-L2 {err:.2e}"
+    finally:
+        for key in (b"gemv_mfma_min_batch", b"gemv_long_kc", b"gemv_long_gpw",
+                    b"gemv_long_stage"):
+            lib.db_tune(key, 0)
+
+
 # --------------------------------------------------- GEMV edge shapes
 # The smallest K (one 16-byte chunk per row), a single output row, and the
 # largest K the ABI accepts (the activation row fills the 152 KB LDS

@@ -5,7 +5,8 @@ draw the rest of the contract at random: every GEMV mode (plain, F1, F2,
 RMSNorm→F2) in fp16 and e4m3 weights with batches that land on both the
 VALU and the MFMA kernel (K ∈ {2048, 4096} is weighted up so the MFMA path
 is hit), ragged K and N, one weight matrix at 17..48 rows (the MFMA kernel's
-32-row passes), and F4 over random batch, head grouping, KV length and
+32-row passes), plain GEMV with K a multiple of 2048 above 4096 at 3..48
+rows (the long-row MFMA kernel), and F4 over random batch, head grouping, KV length and
 split count.  The draws are fixed by the seed, so every run tests the
 same cases; each prints its case before it runs.  DB_RANDOM_SHAPES=<n> and
 DB_RANDOM_SEED=<s> draw a larger or different set for a one-off sweep (the
@@ -90,6 +91,22 @@ def _pass32_cases(n=max(16, N_GEMV // 3), seed=SEED + 2):
     return cases
 
 
+def _long_cases(n=max(16, N_GEMV // 3), seed=SEED + 3):
+    """Plain GEMV at 3..48 rows with K a multiple of 2048 above 4096: the
+    long-row MFMA kernel that streams x in K chunks (one pass up to 32 rows)."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < n:
+        dtype = "fp8" if rng.random() < 0.5 else "f16"
+        B = int(rng.choice([3, 5, 8, 9, 16, 17, 24, 32, 33, 48]))
+        K = 2048 * int(rng.integers(3, 15))
+        N = int(rng.integers(1, 4097))
+        if B * N * K > 8 * MAC_BUDGET:
+            continue
+        cases.append(("plain", dtype, B, K, N, int(rng.integers(1 << 30))))
+    return cases
+
+
 def _f4_cases(n=N_GEMV // 2, seed=SEED + 1):
     rng = np.random.default_rng(seed)
     cases = []
@@ -109,7 +126,7 @@ def _lib():
     cref.load()
 
 
-@pytest.mark.parametrize("mode,dtype,B,K,N,seed", _gemv_cases() + _pass32_cases())
+@pytest.mark.parametrize("mode,dtype,B,K,N,seed", _gemv_cases() + _pass32_cases() + _long_cases())
 def test_random_gemv_shapes(mode, dtype, B, K, N, seed):
     print(f"[rand-gemv] {mode} {dtype} B={B} K={K} N={N} seed={seed}", flush=True)
     gen = torch.Generator().manual_seed(seed)
