@@ -264,6 +264,82 @@ def test_long_row_gemv_launch_shapes_agree():
             lib.db_tune(key, 0)
 
 
+# --------------------------------------------------- gate/up pair, streamed x
+# The gate/up pair + SwiGLU from 17 rows (K a multiple of 2048, N of 8)
+# streams x in K chunks on 4-wave workgroups: 32 rows per pass, the full
+# config-2 shape at B=32 (7 groups per workgroup), a second pass above 32,
+# fewer groups than CUs, fp16 and e4m3; N not a multiple of 8 keeps the
+# 16-row passes.
+PAIR_CASES = [
+    ("f16", 32, 4096, 14336), ("f16", 17, 4096, 2048), ("f16", 40, 2048, 776),
+    ("f16", 24, 4096, 1001), ("f16", 33, 6144, 264),
+    ("fp8", 32, 4096, 14336), ("fp8", 20, 2048, 1792), ("fp8", 48, 4096, 520),
+]
+
+
+@pytest.mark.parametrize("dtype,B,K,N", PAIR_CASES)
+def test_gateup_pair_streamed_parity(dtype, B, K, N):
+    from decodebench_amd.quant import quantize_e4m3_rows
+
+    print(f"[pair] {dtype} B={B} K={K} N={N}", flush=True)
+    gen = torch.Generator().manual_seed(9000 + B + K + N)
+    x = randn(gen, (B, K))
+    Wg = randn(gen, (N, K), std=0.02)
+    Wu = randn(gen, (N, K), std=0.02)
+    if dtype == "fp8":
+        Gq, sg = quantize_e4m3_rows(Wg)
+        Uq, su = quantize_e4m3_rows(Wu)
+        y = ops.f2_gateup_swiglu(x.cuda(), Gq.cuda(), Uq.cuda(), sg.cuda(), su.cuda())
+        ref = stages.f2_fp8(x, Gq, sg, Uq, su)
+        exact = cref.f2_fp8_exact(x.numpy(), Gq.view(torch.uint8).numpy(), sg.numpy(),
+                                  Uq.view(torch.uint8).numpy(), su.numpy())
+    else:
+        y = ops.f2_gateup_swiglu(x.cuda(), Wg.cuda(), Wu.cuda())
+        ref, exact = stages.f2(x, Wg, Wu), cref.f2_exact(x.numpy(), Wg.numpy(), Wu.numpy())
+    torch.cuda.synchronize()
+    assert y.shape == (B, N)
+    assert_parity(y, ref, exact, 5e-3, f"pair {dtype} B={B} K={K} N={N}")
+
+
+def test_gateup_pair_launch_shapes_agree():
+    """The config-2 gate/up pair at 16 and 32 rows through the streamed kernel
+    (every chunk size, both x paths, 1-7 groups per workgroup) and through the
+    16-row passes agrees to fp32 summation order, fp16 and e4m3."""
+    from decodebench_amd.quant import quantize_e4m3_rows
+
+    gen = torch.Generator().manual_seed(80)
+    lib = ops.load_library()
+    Wg = randn(gen, (14336, 4096), std=0.02)
+    Wu = randn(gen, (14336, 4096), std=0.02)
+    Gq, sg = (t.cuda() for t in quantize_e4m3_rows(Wg))
+    Uq, su = (t.cuda() for t in quantize_e4m3_rows(Wu))
+    Wg, Wu = Wg.cuda(), Wu.cuda()
+    keys = (b"gemv_pair_min_batch", b"gemv_long_kc", b"gemv_long_gpw", b"gemv_long_stage",
+            b"gemv_pair_tiles")
+    shapes = [(2, kc, 1, 0) for kc in (2, 4)]  # 16-row tiles
+    shapes += [(1, kc, stage, gpw) for kc, stage in ((1, 1), (2, 1), (2, 2))
+               for gpw in (0, 2, 4, 7)]      # 8-row halves
+    try:
+        for B in (16, 32):
+            x = randn(gen, (B, 4096)).cuda()
+            assert lib.db_tune(b"gemv_pair_min_batch", 1 << 20) == 0
+            base = (ops.f2_gateup_swiglu(x, Wg, Wu), ops.f2_gateup_swiglu(x, Gq, Uq, sg, su))
+            assert lib.db_tune(b"gemv_pair_min_batch", 2) == 0
+            for tiles, kc, stage, gpw in shapes:
+                assert lib.db_tune(b"gemv_pair_tiles", tiles) == 0
+                assert lib.db_tune(b"gemv_long_kc", kc) == 0
+                assert lib.db_tune(b"gemv_long_stage", stage) == 0
+                assert lib.db_tune(b"gemv_long_gpw", gpw) == 0
+                got = (ops.f2_gateup_swiglu(x, Wg, Wu), ops.f2_gateup_swiglu(x, Gq, Uq, sg, su))
+                for a, b in zip(got, base):
+                    err = rel_l2(a.float().cpu().numpy(), b.float().cpu().numpy())
+                    assert err < 1e-3, (f"B={B} tiles={tiles} kc={kc} stage={stage} gpw={gpw}: "
+                                        f"rel-L2 {err:.2e}")
+    finally:
+        for key in keys:
+            lib.db_tune(key, 0)
+
+
 # --------------------------------------------------- GEMV edge shapes
 # The smallest K (one 16-byte chunk per row), a single output row, and the
 # largest K the ABI accepts (the activation row fills the 152 KB LDS
