@@ -353,12 +353,12 @@ int db_tune(const char* key, int value) {
       return fail(DB_ERR_INVALID, "db_tune: f4_depth must be 0, 1 or 2");
     t.f4_depth = value;
   } else if (!strcmp(key, "gemv_long_kc")) {
-    if (value != 0 && value != 1 && value != 2 && value != 4)
-      return fail(DB_ERR_INVALID, "db_tune: gemv_long_kc must be 0, 1, 2 or 4");
+    if (value != 0 && value != 2 && value != 4)
+      return fail(DB_ERR_INVALID, "db_tune: gemv_long_kc must be 0, 2 or 4");
     t.gemv_long_kc = value;
   } else if (!strcmp(key, "gemv_long_gpw")) {
-    if (value != 0 && value != 1 && value != 2 && value != 4 && value != 7)
-      return fail(DB_ERR_INVALID, "db_tune: gemv_long_gpw must be 0, 1, 2, 4 or 7");
+    if (value != 0 && value != 1 && value != 2 && value != 4)
+      return fail(DB_ERR_INVALID, "db_tune: gemv_long_gpw must be 0, 1, 2 or 4");
     t.gemv_long_gpw = value;
   } else if (!strcmp(key, "gemv_long_stage")) {
     if (value < 0 || value > 2)
@@ -368,10 +368,6 @@ int db_tune(const char* key, int value) {
     if (value < 0 || value == 1)
       return fail(DB_ERR_INVALID, "db_tune: gemv_pair_min_batch must be 0 (automatic) or >= 2");
     t.gemv_pair_min_batch = value;
-  } else if (!strcmp(key, "gemv_pair_tiles")) {
-    if (value < 0 || value > 2)
-      return fail(DB_ERR_INVALID, "db_tune: gemv_pair_tiles must be 0, 1 or 2");
-    t.gemv_pair_tiles = value;
   } else if (!strcmp(key, "f4_min_tiles")) {
     if (value < 1) return fail(DB_ERR_INVALID, "db_tune: f4_min_tiles must be >= 1");
     t.f4_min_tiles = value;

@@ -22,12 +22,10 @@ struct Tuning {
   int f4_line = 0;             // F4 score layout: 0 auto, 1 whole-line K loads, 2 plain
   int f4_combine_groups = 0;   // split groups per F4 merge workgroup (0: auto)
   int f4_depth = 0;            // F4 tiles in flight per wave: 0 auto, 1 or 2
-  int gemv_long_kc = 0;        // long-row MFMA GEMV k-steps per chunk: 0 auto, 2 or 4
+  int gemv_long_kc = 0;        // streamed-x MFMA GEMV k-steps per chunk: 0 auto, 2 or 4
   int gemv_long_gpw = 0;       // long-row MFMA GEMV row groups per workgroup: 0 auto, 1, 2, 4
   int gemv_long_stage = 0;     // long-row MFMA GEMV x: 0 auto, 1 direct, 2 LDS-staged
   int gemv_pair_min_batch = 0; // gate/up pair rows from which x streams (0: 17)
-  int gemv_pair_tiles = 0;     // gate/up pair, streamed x: 0 auto (fp16 1, e4m3 2),
-                               // 1 8-row halves, 2 16-row tiles
 };
 Tuning& tuning();
 

@@ -38,8 +38,7 @@
 // to the partial sums (XB), otherwise passes are 16 rows.
 // Plain GEMV with longer rows (K a multiple of 2048 above 4096, the down
 // projection) and the gate/up pair above 16 rows take kernels that stream x
-// as well: gemv_mfma_long_kernel, and for the e4m3 pair
-// gemv_mfma_tile16_kernel.
+// as well: gemv_mfma_long_kernel and gemv_mfma_tile16_kernel.
 #include "gemv_valu.h"
 
 namespace dbk {
@@ -472,41 +471,34 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   }
 }
 
-// ---- streamed activations: long rows, and the gate/up pair above 16 rows ---
+// ---- long rows: K a multiple of 2048 above 4096 ---------------------------
 // At K = 14336 (the down projection) a 16-row activation slice would take
-// 224 VGPRs, and 32 rows of the gate/up pair's x at K = 4096 would take 128
-// KB of LDS beside the pair's partial sums, so here both operands stream.
-// Wave v of workgroup w owns an XCD-staggered K / WV slice (as above) and
-// walks it in chunks of KC k-steps (64 KC columns, dealt out over the halves
-// and lane groups as above).  Per chunk it loads the pass's BT batch tiles
-// of x and the chunk of each of the workgroup's GPW groups (of each of the
-// NWM matrices), and the MFMA sums accumulate in registers across chunks;
-// two register sets alternate (load chunk c + 1, consume chunk c).  Batch
-// rows past the batch read x's last row and rows past N read W's last row:
-// batch column n of an MFMA sees only x row n and output row m only weight
-// row m, and those columns and rows are never stored.  No norm modes: a
-// norm would need all of x before the first product.
-// The gate/up pair runs 4-wave workgroups (one wave per SIMD), so that a
-// wave's accumulators for the 7 groups x 2 matrices x 32 batch rows of
-// N = 14336 (224 registers) fit beside its weight sets.
+// 224 VGPRs, so here both operands stream.  Wave v of workgroup w owns the
+// same XCD-staggered K / 8 slice as above and walks it in chunks of KC
+// k-steps (64 KC columns, dealt out over the halves and lane groups as
+// above).  Per chunk it loads the pass's BT batch tiles of x and the chunk
+// of each of the workgroup's GPW groups, and the MFMA sums accumulate in
+// registers across chunks; two register sets alternate (load chunk c + 1,
+// consume chunk c).  Batch rows past the batch read x's last row and rows
+// past N read W's last row: batch column n of an MFMA sees only x row n and
+// output row m only weight row m, and those columns and rows are never
+// stored.  Plain GEMV only: a norm would need all of x before the first
+// product.
 // XS: x is loaded contiguously -- lane l takes 16-byte piece l % 8 KC of
 // the chunk of batch row l / 8 KC, 64 / (8 KC) rows per instruction -- and
 // staged through the wave's LDS tile (the xslot layout) into B operands;
 // otherwise each lane loads its own B operands (8 batch rows x 128 bytes
 // per instruction).
-template <int NWM, int WV, int KC, int BT, int GPW, bool FP8, bool XS>
-__global__ __launch_bounds__(WV * kWave) void gemv_mfma_long_kernel(MfmaArgs a) {
-  constexpr int kThreads = WV * kWave;
+template <int KC, int BT, int GPW, bool FP8, bool XS>
+__global__ __launch_bounds__(kThreadsM) void gemv_mfma_long_kernel(MfmaArgs a) {
   constexpr int KWC = FP8 ? KC / 2 : KC;  // 16-byte weight loads per row and chunk
   constexpr int kPass = 8 * BT;
   constexpr int kXL = BT * KC;            // x loads per chunk, either way
   static_assert(!FP8 || KC % 2 == 0, "an e4m3 load spans two k-steps");
-  static_assert((WV & (WV - 1)) == 0, "waves per workgroup: a power of 2");
-  // Dynamic LDS: XS, each wave's x tile [batch tile][k-step][slot] (BT KC
-  // KB per wave); then the partial sums [group][matrix][wave][batch][row].
+  // [group][wave][batch][row quad]: rows 4 i .. 4 i + 3 of a group
+  __shared__ f4 part[GPW][kWavesM][kPass][2];
+  // XS: each wave's x tile, [batch tile][k-step][slot] (BT KC KB per wave)
   extern __shared__ __align__(16) unsigned char dyn_lds[];
-  float* const part =
-      reinterpret_cast<float*>(dyn_lds + (XS ? (size_t)WV * kXL * kWave * 16 : 0));
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -517,9 +509,9 @@ __global__ __launch_bounds__(WV * kWave) void gemv_mfma_long_kernel(MfmaArgs a) 
   const int bx = blockIdx.x;
   const int b0 = blockIdx.y * kPass;
   const int nb = min(kPass, a.B - b0);
-  const int slice = a.K / WV;
+  const int slice = a.K / kWavesM;
   const int nch = slice / (64 * KC);
-  const int sbase = ((wave + bx + (bx >> 3)) & (WV - 1)) * slice;
+  const int sbase = ((wave + bx + (bx >> 3)) & (kWavesM - 1)) * slice;
   // This lane's first column: fp16 k-step t of chunk c covers
   // 64 (KC c + t) + 32 h + 8 g4; e4m3 load p covers 64 KC c + 128 p + 64 h
   // + 16 g4 (k-steps 2p and 2p + 1, x 8 columns apart).
@@ -565,44 +557,23 @@ __global__ __launch_bounds__(WV * kWave) void gemv_mfma_long_kernel(MfmaArgs a) 
       xp[bt] = a.x + (size_t)(b0 + min(8 * bt + r8, nb - 1)) * a.K + lcol;
   }
   u4* const tile = reinterpret_cast<u4*>(dyn_lds) + (size_t)wave * kXL * kWave;
-  const unsigned char* wmat[2] = {static_cast<const unsigned char*>(a.w0),
-                                  static_cast<const unsigned char*>(a.w1)};
-  // Weights.  One matrix: a pointer per group, its rows clamped to N - 1.
-  // The pair (launched with N a multiple of 8 and N K bytes below 4 GiB, so
-  // every row of a live group is below N): one 32-bit lane offset, and a
-  // wave-uniform base per group and matrix, which keeps 14 pointers out of
-  // the registers the 7-group accumulators need.
-  constexpr bool kLaneOffset = NWM == 2;
+  const unsigned char* wp[GPW];
   const int esz = FP8 ? 1 : 2;
-  const unsigned char* wp[kLaneOffset ? 1 : GPW];
-  unsigned woff = 0;
-  if constexpr (kLaneOffset) {
-    woff = ((unsigned)(bx * kRowsPerGroup + r8) * (unsigned)a.K + (unsigned)lcol) * esz;
-  } else {
 #pragma unroll
-    for (int q = 0; q < GPW; ++q) {
-      const int grp = bx + (int)gridDim.x * min(q, my_groups - 1);
-      const int row = min(grp * kRowsPerGroup + r8, a.N - 1);
-      wp[q] = wmat[0] + ((size_t)row * a.K + lcol) * esz;
-    }
+  for (int q = 0; q < GPW; ++q) {
+    const int grp = bx + (int)gridDim.x * min(q, my_groups - 1);
+    const int row = min(grp * kRowsPerGroup + r8, a.N - 1);
+    wp[q] = static_cast<const unsigned char*>(a.w0) + ((size_t)row * a.K + lcol) * esz;
   }
-  const size_t gstride = (size_t)gridDim.x * kRowsPerGroup * a.K * esz;
   auto xoff = [](int t) { return FP8 ? 128 * (t >> 1) + 8 * (t & 1) : 64 * t; };
 
-  auto load = [&](u4 (&xs)[kXL], u4 (&ws)[GPW][NWM][KWC], int c) {
+  auto load = [&](u4 (&xs)[kXL], u4 (&ws)[GPW][KWC], int c) {
     const int c0 = 64 * KC * c;
 #pragma unroll
     for (int q = 0; q < GPW; ++q)
 #pragma unroll
-      for (int m = 0; m < NWM; ++m)
-#pragma unroll
-        for (int p = 0; p < KWC; ++p) {
-          const size_t koff = (size_t)(c0 + 64 * p * (FP8 ? 2 : 1)) * esz;
-          if constexpr (kLaneOffset)
-            ws[q][m][p] = ld_stream(wmat[m] + gstride * min(q, my_groups - 1) + koff + woff);
-          else
-            ws[q][m][p] = ld_stream(wp[q] + koff);
-        }
+      for (int p = 0; p < KWC; ++p)
+        ws[q][p] = ld_stream(wp[q] + (size_t)(c0 + 64 * p * (FP8 ? 2 : 1)) * esz);
     if constexpr (XS) {
       const unsigned char* xc = reinterpret_cast<const unsigned char*>(xp[0] + c0);
 #pragma unroll
@@ -612,14 +583,12 @@ __global__ __launch_bounds__(WV * kWave) void gemv_mfma_long_kernel(MfmaArgs a) 
       for (int i = 0; i < kXL; ++i) xs[i] = ld16(xp[i / KC] + c0 + xoff(i % KC));
     }
   };
-  f4 acc[GPW][NWM][BT];
+  f4 acc[GPW][BT];
 #pragma unroll
   for (int q = 0; q < GPW; ++q)
 #pragma unroll
-    for (int m = 0; m < NWM; ++m)
-#pragma unroll
-      for (int bt = 0; bt < BT; ++bt) acc[q][m][bt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-  auto consume = [&](const u4 (&xl)[kXL], const u4 (&ws)[GPW][NWM][KWC]) {
+    for (int bt = 0; bt < BT; ++bt) acc[q][bt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  auto consume = [&](const u4 (&xl)[kXL], const u4 (&ws)[GPW][KWC]) {
     u4 xs[kXL];
     if constexpr (XS) {
       // A wave's LDS accesses complete in order: the previous chunk's reads
@@ -637,30 +606,29 @@ __global__ __launch_bounds__(WV * kWave) void gemv_mfma_long_kernel(MfmaArgs a) 
 #pragma unroll
       for (int i = 0; i < kXL; ++i) xs[i] = xl[i];
     }
-    // One weight load at a time (two k-steps of e4m3, widened here, one of
-    // fp16) against every batch tile, groups and matrices interleaved.
-    constexpr int kStepsPerLoad = FP8 ? 2 : 1;
+    u4 av[GPW][KC];
 #pragma unroll
-    for (int p = 0; p < KWC; ++p)
+    for (int q = 0; q < GPW; ++q) {
+      if constexpr (FP8) {
+#pragma unroll
+        for (int p = 0; p < KWC; ++p) e4m3x16_to_h(ws[q][p], av[q][2 * p], av[q][2 * p + 1]);
+      } else {
+#pragma unroll
+        for (int t = 0; t < KC; ++t) av[q][t] = ws[q][t];
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < KC; ++t)
 #pragma unroll
       for (int q = 0; q < GPW; ++q)
 #pragma unroll
-        for (int m = 0; m < NWM; ++m) {
-          u4 av[kStepsPerLoad];
-          if constexpr (FP8) e4m3x16_to_h(ws[q][m][p], av[0], av[1]);
-          else av[0] = ws[q][m][p];
-#pragma unroll
-          for (int j = 0; j < kStepsPerLoad; ++j)
-#pragma unroll
-            for (int bt = 0; bt < BT; ++bt)
-              acc[q][m][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                  __builtin_bit_cast(h8, av[j]),
-                  __builtin_bit_cast(h8, xs[bt * KC + kStepsPerLoad * p + j]), acc[q][m][bt], 0,
-                  0, 0);
-        }
+        for (int bt = 0; bt < BT; ++bt)
+          acc[q][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              __builtin_bit_cast(h8, av[q][t]), __builtin_bit_cast(h8, xs[bt * KC + t]),
+              acc[q][bt], 0, 0, 0);
   };
 
-  u4 xa[kXL], wa[GPW][NWM][KWC], xb[kXL], wb[GPW][NWM][KWC];
+  u4 xa[kXL], wa[GPW][KWC], xb[kXL], wb[GPW][KWC];
   load(xa, wa, 0);
   int c = 0;
   for (; c + 3 <= nch; c += 2) {
@@ -676,46 +644,30 @@ __global__ __launch_bounds__(WV * kWave) void gemv_mfma_long_kernel(MfmaArgs a) 
 
   // D[4 g4 + i][c16]: rows 0..7 x batch 0..7 (half 0) in lanes (g4 < 2,
   // c16 < 8), their half-1 partners 40 lanes higher.
-  auto slot = [&](int q, int m, int v, int n) {
-    return part + ((((q * NWM + m) * WV + v) * kPass + n) * kRowsPerGroup);
-  };
 #pragma unroll
   for (int q = 0; q < GPW; ++q)
 #pragma unroll
-    for (int m = 0; m < NWM; ++m)
+    for (int bt = 0; bt < BT; ++bt) {
+      f4 v = acc[q][bt];
 #pragma unroll
-      for (int bt = 0; bt < BT; ++bt) {
-        f4 v = acc[q][m][bt];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] += __shfl(v[i], lane + 40);
-        if (g4 < 2 && c16 < 8) *reinterpret_cast<f4*>(slot(q, m, wave, 8 * bt + c16) + 4 * g4) = v;
-      }
+      for (int i = 0; i < 4; ++i) v[i] += __shfl(v[i], lane + 40);
+      if (g4 < 2 && c16 < 8) part[q][wave][8 * bt + c16][g4] = v;
+    }
   __syncthreads();
 
-  // ---- reduce the K-slices, row scales, epilogue, fp16 store -------------
-  for (int idx = threadIdx.x; idx < my_groups * kPass * kRowsPerGroup; idx += kThreads) {
+  // ---- reduce the 8 K-slices, row scales, fp16 store ---------------------
+  const float* pf = reinterpret_cast<const float*>(&part[0][0][0][0]);
+  for (int idx = threadIdx.x; idx < my_groups * kPass * kRowsPerGroup; idx += kThreadsM) {
     const int q = idx / (kPass * kRowsPerGroup);
     const int n = (idx / kRowsPerGroup) % kPass;
     const int r = idx % kRowsPerGroup;
     const int row = (bx + (int)gridDim.x * q) * kRowsPerGroup + r;
     if (n >= nb || row >= a.N) continue;
-    float s0 = 0.0f, s1 = 0.0f;
+    float s = 0.0f;
 #pragma unroll
-    for (int v = 0; v < WV; ++v) {
-      s0 += slot(q, 0, v, n)[r];
-      if constexpr (NWM == 2) s1 += slot(q, NWM - 1, v, n)[r];
-    }
-    if constexpr (FP8) {
-      s0 *= a.s0[row];
-      if constexpr (NWM == 2) s1 *= a.s1[row];
-    }
-    float out = s0;
-    if constexpr (NWM == 2) {
-      const float gq = (float)to_h(s0);
-      const float uq = (float)to_h(s1);
-      out = (float)to_h(gemv_silu(gq)) * uq;
-    }
-    a.y[(size_t)(b0 + n) * a.N + row] = to_h(out);
+    for (int v = 0; v < kWavesM; ++v) s += pf[((q * kWavesM + v) * kPass + n) * kRowsPerGroup + r];
+    if constexpr (FP8) s *= a.s0[row];
+    a.y[(size_t)(b0 + n) * a.N + row] = to_h(s);
   }
 }
 
@@ -723,28 +675,56 @@ __global__ __launch_bounds__(WV * kWave) void gemv_mfma_long_kernel(MfmaArgs a) 
 // The kernel above spends three quarters of every accumulator: an 8-row
 // group over two half slices fills one v_mfma_f32_16x16x32_f16, but only
 // its two diagonal 8 x 8 blocks are dot products.  For the gate/up pair at
-// 32 rows that is 7 groups x 2 matrices x 4 tiles of accumulators (224
-// registers) on a CU's 56 rows, and the register allocator then shuffles
-// accumulators through a shared temporary between MFMAs.  Here an MFMA
+// 32 rows that would be 7 groups x 2 matrices x 4 tiles of accumulators
+// (224 registers) on a CU's 56 rows; a version built that way had the
+// register allocator move accumulators through a shared temporary between
+// MFMAs and ran 1.5x slower (e4m3).  Here an MFMA
 // takes 16 weight rows (two of the workgroup's 8-row groups) against 16
 // batch rows over the same 32 columns, and every element of D is an output:
 // A row m = row m & 7 of group 2j + (m >> 3), k-group g4 = columns
-// 32 t + 8 g4 (fp16) or, for e4m3, load p = columns 64 p + 16 g4 (k-steps
-// 2p and 2p + 1, x 8 columns apart); B column n = batch row 16 bt + n.
-// A load instruction then reads 16 rows x 64 bytes.  Waves own K / WV
-// slices as above and walk them in chunks of KC k-steps; accumulators stay
-// in registers; the K-slice partial sums meet in LDS with the same layout
-// and epilogue as above.  A workgroup owns up to 2 T groups; a last tile
-// with one group duplicates it in rows 8..15, which are not stored.
-// Launched with N a multiple of 8 and N K bytes below 4 GiB (32-bit lane
-// offsets, every row of a live group below N).
+// 32 s + 8 g4 of k-step s (fp16) or, for e4m3, columns 64 (s >> 1) +
+// 16 g4 + 8 (s & 1); B column n = batch row 16 bt + n over the same columns.
+// Loading those A operands directly would read 16 rows x 64 bytes (half
+// lines) per instruction.  Instead each 8-row group is loaded as above --
+// lane (g4, h, r8) takes row r8, half h of a 128-byte line, 8 whole lines
+// per instruction -- and the two groups of a tile are merged into its A
+// operands with one DPP row_ror:8 move per register: lanes 8..15 of each
+// 16-lane row of the first group's register take lanes 0..7 of the
+// second's (the tile's half-0 operand), and lanes 0..7 of the second's take
+// lanes 8..15 of the first's (its half-1 operand).
+// Waves own K / WV slices as above and walk them in chunks of KC k-steps;
+// accumulators stay in registers; the K-slice partial sums meet in LDS with
+// the same layout and epilogue as above.  A workgroup owns up to 2 T
+// groups; a last tile with one group duplicates it in rows 8..15, which are
+// not stored.  Launched with N a multiple of 8 and 2 N K bytes below 4 GiB
+// (32-bit lane offsets; every row of a live group below N).
+__device__ __forceinline__ u4 tile_half0(const u4& g0, const u4& g1) {
+  u4 t;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    t[i] = (unsigned)__builtin_amdgcn_update_dpp((int)g0[i], (int)g1[i], kRowRor8, 0xf, 0xc,
+                                                 false);
+  return t;
+}
+__device__ __forceinline__ u4 tile_half1(const u4& g0, const u4& g1) {
+  u4 t;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    t[i] = (unsigned)__builtin_amdgcn_update_dpp((int)g1[i], (int)g0[i], kRowRor8, 0xf, 0x3,
+                                                 false);
+  return t;
+}
+
 template <int NWM, int WV, int KC, int BT16, int T, bool FP8>
 __global__ __launch_bounds__(WV * kWave) void gemv_mfma_tile16_kernel(MfmaArgs a) {
   constexpr int kThreads = WV * kWave;
-  constexpr int KWC = FP8 ? KC / 2 : KC;
+  constexpr int kStepsPerLoad = FP8 ? 2 : 1;  // k-steps in a 16-byte A operand
+  constexpr int LS = 2 * kStepsPerLoad;       // k-steps per line load (both halves)
+  static_assert(KC % LS == 0, "a chunk holds whole lines");
+  constexpr int KWC = KC / LS;                // line loads per group and chunk
+  constexpr int NG = 2 * T;                   // 8-row groups
   constexpr int kPass = 16 * BT16;
   constexpr int kXL = BT16 * KC;
-  static_assert(!FP8 || KC % 2 == 0, "an e4m3 load spans two k-steps");
   static_assert((WV & (WV - 1)) == 0, "waves per workgroup: a power of 2");
   extern __shared__ __align__(16) unsigned char dyn_lds[];
   float* const part = reinterpret_cast<float*>(dyn_lds);  // [2T][NWM][WV][kPass][8]
@@ -760,41 +740,40 @@ __global__ __launch_bounds__(WV * kWave) void gemv_mfma_tile16_kernel(MfmaArgs a
   const int slice = a.K / WV;
   const int nch = slice / (32 * KC);  // chunks of KC k-steps of 32 columns
   const int sbase = ((wave + bx + (bx >> 3)) & (WV - 1)) * slice;
-  const int lcol = sbase + (FP8 ? 16 * g4 : 8 * g4);
+  const int xcol0 = sbase + (FP8 ? 16 * g4 : 8 * g4);
   const int my_groups = min(a.gpw, (a.groups - bx + grid - 1) / grid);
   const int esz = FP8 ? 1 : 2;
-
-  // Weight lane offsets: rows of group pair (2j, 2j + 1), and for a tile
-  // whose second group does not exist, group 2j in both halves.
-  const unsigned row_pair = (unsigned)(bx * kRowsPerGroup + (c16 & 7) +
-                                       (c16 >> 3) * grid * kRowsPerGroup);
-  const unsigned row_one = (unsigned)(bx * kRowsPerGroup + (c16 & 7));
-  const unsigned woff_pair = (row_pair * (unsigned)a.K + (unsigned)lcol) * esz;
-  const unsigned woff_one = (row_one * (unsigned)a.K + (unsigned)lcol) * esz;
-  const size_t tstride = (size_t)2 * grid * kRowsPerGroup * a.K * esz;  // one tile further
   const unsigned char* wmat[2] = {static_cast<const unsigned char*>(a.w0),
                                   static_cast<const unsigned char*>(a.w1)};
+
+  // Weight lane offset: row r8 of the group, half h of the line; groups are
+  // gstride apart (group q of the workgroup is bx + grid q).
+  const int r8 = c16 & 7;
+  const int half = c16 >> 3;
+  const int wcol0 = sbase + (FP8 ? 64 * half + 16 * g4 : 32 * half + 8 * g4);
+  const unsigned woff = ((unsigned)(bx * kRowsPerGroup + r8) * (unsigned)a.K +
+                         (unsigned)wcol0) * esz;
+  const size_t gstride = (size_t)grid * kRowsPerGroup * a.K * esz;
   const _Float16* xp[BT16];
 #pragma unroll
   for (int bt = 0; bt < BT16; ++bt)
-    xp[bt] = a.x + (size_t)(b0 + min(16 * bt + c16, nb - 1)) * a.K + lcol;
-  // Column offset of k-step t (fp16) or load p (e4m3) within a chunk.
-  auto wcol = [](int p) { return FP8 ? 64 * p : 32 * p; };
+    xp[bt] = a.x + (size_t)(b0 + min(16 * bt + c16, nb - 1)) * a.K + xcol0;
+  // Column offset of line load p within a chunk, and of k-step t's
+  // activations.
+  auto wcol = [](int p) { return (FP8 ? 128 : 64) * p; };
   auto xcol = [](int t) { return FP8 ? 64 * (t >> 1) + 8 * (t & 1) : 32 * t; };
 
-  auto load = [&](u4 (&xs)[kXL], u4 (&ws)[T][NWM][KWC], int c) {
+  auto load = [&](u4 (&xs)[kXL], u4 (&ws)[NG][NWM][KWC], int c) {
     const int c0 = 32 * KC * c;
 #pragma unroll
-    for (int j = 0; j < T; ++j) {
-      // Tiles past the workgroup's groups re-read its first tile.
-      const int jj = 2 * j < my_groups ? j : 0;
-      const bool pair = 2 * jj + 1 < my_groups;
+    for (int j = 0; j < NG; ++j) {
+      // Groups past the workgroup's last re-read that one (rows not stored).
+      const size_t goff = gstride * min(j, my_groups - 1);
 #pragma unroll
       for (int m = 0; m < NWM; ++m)
 #pragma unroll
         for (int p = 0; p < KWC; ++p)
-          ws[j][m][p] = ld_stream(wmat[m] + tstride * jj + (size_t)(c0 + wcol(p)) * esz +
-                                  (pair ? woff_pair : woff_one));
+          ws[j][m][p] = ld_stream(wmat[m] + goff + (size_t)(c0 + wcol(p)) * esz + woff);
     }
 #pragma unroll
     for (int i = 0; i < kXL; ++i) xs[i] = ld16(xp[i / KC] + c0 + xcol(i % KC));
@@ -806,29 +785,34 @@ __global__ __launch_bounds__(WV * kWave) void gemv_mfma_tile16_kernel(MfmaArgs a
     for (int m = 0; m < NWM; ++m)
 #pragma unroll
       for (int bt = 0; bt < BT16; ++bt) acc[j][m][bt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-  auto consume = [&](const u4 (&xs)[kXL], const u4 (&ws)[T][NWM][KWC]) {
-    constexpr int kStepsPerLoad = FP8 ? 2 : 1;
+  // A operand u (16 bytes, kStepsPerLoad k-steps from k-step t0) of tile j.
+  auto mma = [&](const u4& u, int j, int m, int t0, const u4 (&xs)[kXL]) {
+    u4 av[kStepsPerLoad];
+    if constexpr (FP8) e4m3x16_to_h(u, av[0], av[1]);
+    else av[0] = u;
+#pragma unroll
+    for (int s = 0; s < kStepsPerLoad; ++s)
+#pragma unroll
+      for (int bt = 0; bt < BT16; ++bt)
+        acc[j][m][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            __builtin_bit_cast(h8, av[s]), __builtin_bit_cast(h8, xs[bt * KC + t0 + s]),
+            acc[j][m][bt], 0, 0, 0);
+  };
+  auto consume = [&](const u4 (&xs)[kXL], const u4 (&ws)[NG][NWM][KWC]) {
 #pragma unroll
     for (int p = 0; p < KWC; ++p)
 #pragma unroll
       for (int j = 0; j < T; ++j)
 #pragma unroll
         for (int m = 0; m < NWM; ++m) {
-          u4 av[kStepsPerLoad];
-          if constexpr (FP8) e4m3x16_to_h(ws[j][m][p], av[0], av[1]);
-          else av[0] = ws[j][m][p];
-#pragma unroll
-          for (int s = 0; s < kStepsPerLoad; ++s)
-#pragma unroll
-            for (int bt = 0; bt < BT16; ++bt)
-              acc[j][m][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                  __builtin_bit_cast(h8, av[s]),
-                  __builtin_bit_cast(h8, xs[bt * KC + kStepsPerLoad * p + s]), acc[j][m][bt], 0,
-                  0, 0);
+          const u4& g0 = ws[2 * j][m][p];
+          const u4& g1 = ws[2 * j + 1][m][p];
+          mma(tile_half0(g0, g1), j, m, LS * p, xs);
+          mma(tile_half1(g0, g1), j, m, LS * p + kStepsPerLoad, xs);
         }
   };
 
-  u4 xa[kXL], wa[T][NWM][KWC], xb[kXL], wb[T][NWM][KWC];
+  u4 xa[kXL], wa[NG][NWM][KWC], xb[kXL], wb[NG][NWM][KWC];
   load(xa, wa, 0);
   int c = 0;
   for (; c + 3 <= nch; c += 2) {
@@ -938,9 +922,9 @@ MfmaFn pick_mode(GemvMode mode, int kh, int bt, int ups, bool xb) {
 template <int KC, int BT, bool FP8, bool XS>
 MfmaFn pick_long_gpw(int gpw) {
   constexpr int KC4 = KC == 4 && BT == 4 ? 2 : KC;
-  return gpw == 1 ? gemv_mfma_long_kernel<1, kWavesM, KC, BT, 1, FP8, XS>
-                  : gpw == 2 ? gemv_mfma_long_kernel<1, kWavesM, KC, BT, 2, FP8, XS>
-                             : gemv_mfma_long_kernel<1, kWavesM, KC4, BT, 4, FP8, XS>;
+  return gpw == 1 ? gemv_mfma_long_kernel<KC, BT, 1, FP8, XS>
+                  : gpw == 2 ? gemv_mfma_long_kernel<KC, BT, 2, FP8, XS>
+                             : gemv_mfma_long_kernel<KC4, BT, 4, FP8, XS>;
 }
 
 template <int KC, bool FP8, bool XS>
@@ -960,52 +944,24 @@ MfmaFn pick_long(int kc, int bt, int gpw, bool xs) {
   return xs ? pick_long_kc<FP8, true>(kc, bt, gpw) : pick_long_kc<FP8, false>(kc, bt, gpw);
 }
 
-// The gate/up pair on 4-wave workgroups: 1, 2, 4 or 7 groups per workgroup
-// (7 covers N = 14336 on 256 CUs), batch tiles 2 or 4.
+// The gate/up pair on 16-row tiles: 4 waves, 2 (fp16) or 4 (e4m3, whose
+// whole lines span 4 k-steps) k-steps per chunk, 16 or 32 batch rows, 1, 2
+// or 4 tiles (2, 4 or 8 groups).
 constexpr int kPairWaves = 4;
 
-// fp16 with 2-k-step chunks at 7 groups x 32 rows would spill (both register
-// files full); that combination takes 1-k-step chunks loaded as B operands.
-template <int KC, int BT, bool FP8, bool XS>
-MfmaFn pick_pair_gpw(int gpw) {
-  constexpr bool kSpill7 = !FP8 && KC == 2 && BT == 4;
-  return gpw == 1 ? gemv_mfma_long_kernel<2, kPairWaves, KC, BT, 1, FP8, XS>
-         : gpw == 2 ? gemv_mfma_long_kernel<2, kPairWaves, KC, BT, 2, FP8, XS>
-         : gpw == 4 ? gemv_mfma_long_kernel<2, kPairWaves, KC, BT, 4, FP8, XS>
-                    : gemv_mfma_long_kernel<2, kPairWaves, kSpill7 ? 1 : KC, BT, 7, FP8,
-                                            kSpill7 ? false : XS>;
-}
-
-template <int KC, bool FP8, bool XS>
-MfmaFn pick_pair_bt(int bt, int gpw) {
-  return bt == 2 ? pick_pair_gpw<KC, 2, FP8, XS>(gpw) : pick_pair_gpw<KC, 4, FP8, XS>(gpw);
-}
-
-// fp16: 1-k-step chunks loaded as B operands, or 2-k-step chunks either way;
-// e4m3: 2-k-step chunks (one load spans two k-steps).
-template <bool FP8>
-MfmaFn pick_pair(int kc, int bt, int gpw, bool xs) {
-  if constexpr (FP8) {
-    return xs ? pick_pair_bt<2, true, true>(bt, gpw) : pick_pair_bt<2, true, false>(bt, gpw);
-  } else {
-    if (kc == 1) return pick_pair_bt<1, false, false>(bt, gpw);
-    return xs ? pick_pair_bt<2, false, true>(bt, gpw) : pick_pair_bt<2, false, false>(bt, gpw);
-  }
-}
-
-// Full 16-row tiles for the gate/up pair: 4 waves, 2 or 4 k-steps per
-// chunk, 16 or 32 batch rows, 1, 2 or 4 tiles (2, 4 or 8 groups).
 template <int KC, int BT16, bool FP8>
-MfmaFn pick_tile16_t(int t) {
+MfmaFn pick_pair_t(int t) {
   return t == 1 ? gemv_mfma_tile16_kernel<2, kPairWaves, KC, BT16, 1, FP8>
          : t == 2 ? gemv_mfma_tile16_kernel<2, kPairWaves, KC, BT16, 2, FP8>
                   : gemv_mfma_tile16_kernel<2, kPairWaves, KC, BT16, 4, FP8>;
 }
 
 template <bool FP8>
-MfmaFn pick_tile16(int kc, int bt16, int t) {
-  if (kc == 4) return bt16 == 1 ? pick_tile16_t<4, 1, FP8>(t) : pick_tile16_t<4, 2, FP8>(t);
-  return bt16 == 1 ? pick_tile16_t<2, 1, FP8>(t) : pick_tile16_t<2, 2, FP8>(t);
+MfmaFn pick_pair(int kc, int bt16, int t) {
+  if constexpr (!FP8) {
+    if (kc == 2) return bt16 == 1 ? pick_pair_t<2, 1, FP8>(t) : pick_pair_t<2, 2, FP8>(t);
+  }
+  return bt16 == 1 ? pick_pair_t<4, 1, FP8>(t) : pick_pair_t<4, 2, FP8>(t);
 }
 
 }  // namespace
@@ -1045,7 +1001,6 @@ static hipError_t launch_gemv_mfma_long(const MfmaArgs& a0, bool fp8, int cu_cou
   // at 32 rows the 4-k-step sets spill.
   int kc = tuning().gemv_long_kc;
   if (kc == 0) kc = fp8 && bt == 1 ? 4 : 2;
-  if (kc != 2) kc = 4;  // the chunk sizes instantiated for one matrix
   int gpw = tuning().gemv_long_gpw;
   if (gpw == 0) {
     gpw = 4;
@@ -1055,14 +1010,12 @@ static hipError_t launch_gemv_mfma_long(const MfmaArgs& a0, bool fp8, int cu_cou
         break;
       }
   }
-  if (gpw == 7) gpw = 4;
   a.gpw = gpw;
   const int grid = (a.groups + gpw - 1) / gpw;
   if (bt == 4 && gpw == 4) kc = 2;
   const bool xs = tuning().gemv_long_stage != 1;
   const MfmaFn fn = fp8 ? pick_long<true>(kc, bt, gpw, xs) : pick_long<false>(kc, bt, gpw, xs);
-  const size_t lds = (xs ? (size_t)kWavesM * bt * kc * kWave * 16 : 0) +
-                     sizeof(float) * gpw * kWavesM * 8 * bt * kRowsPerGroup;
+  const size_t lds = xs ? (size_t)kWavesM * bt * kc * kWave * 16 : 0;
   if (lds > 48 * 1024) {
     hipError_t e = allow_large_lds(reinterpret_cast<const void*>(fn), lds);
     if (e != hipSuccess) return e;
@@ -1072,75 +1025,36 @@ static hipError_t launch_gemv_mfma_long(const MfmaArgs& a0, bool fp8, int cu_cou
   return hipGetLastError();
 }
 
-static hipError_t launch_gemv_mfma_tile16(const MfmaArgs& a0, bool fp8, int cu_count,
-                                          hipStream_t stream) {
+// The gate/up pair from 17 rows, measured at [14336, 4096] (µs, graph back to
+// back; 16-row passes / streamed on 8-row halves / on 16-row tiles loaded
+// directly / on 16-row tiles merged from whole lines): fp16 B = 17 74.1 /
+// 43.5 / 53.0 / 39.7, B = 32 76.2 / 44.4 / 55.1 / 42.0; e4m3 B = 17 40.5 /
+// 43.7 / 29.3 / 25.5, B = 32 42.4 / 45.3 / 32.0 / 28.1.  The halves hold
+// four times the accumulators (the register allocator then moved them
+// through a shared temporary between MFMAs); the direct tiles read half
+// lines.  4-k-step fp16 chunks measured 1.5-2.3 us slower, 8-wave
+// workgroups 5-6 us slower.
+static hipError_t launch_gemv_mfma_pair(const MfmaArgs& a0, bool fp8, int cu_count,
+                                        hipStream_t stream) {
   MfmaArgs a = a0;
   // The kernel's 32-bit lane offsets (see gemv_mfma_tile16_kernel).
   if (a.N % kRowsPerGroup != 0 ||
       (size_t)2 * a.N * a.K * (fp8 ? 1 : 2) >= ((size_t)1 << 32))
     return hipErrorInvalidValue;
   const int bt16 = a.B <= 16 ? 1 : 2;  // passes of 16 or 32 rows
-  const int kc = tuning().gemv_long_kc == 2 ? 2 : 4;
+  const int kc = fp8 || tuning().gemv_long_kc == 4 ? 4 : 2;
   int gpw = (a.groups + cu_count - 1) / cu_count;
   if (gpw > 8) gpw = 8;
   const int t = gpw <= 2 ? 1 : gpw <= 4 ? 2 : 4;
   a.gpw = gpw;
   const int grid = (a.groups + gpw - 1) / gpw;
-  const MfmaFn fn = fp8 ? pick_tile16<true>(kc, bt16, t) : pick_tile16<false>(kc, bt16, t);
+  const MfmaFn fn = fp8 ? pick_pair<true>(kc, bt16, t) : pick_pair<false>(kc, bt16, t);
   const size_t lds = sizeof(float) * 2 * t * 2 * kPairWaves * 16 * bt16 * kRowsPerGroup;
   if (lds > 48 * 1024) {
     hipError_t e = allow_large_lds(reinterpret_cast<const void*>(fn), lds);
     if (e != hipSuccess) return e;
   }
   dim3 g(grid, (a.B + 16 * bt16 - 1) / (16 * bt16));
-  hipLaunchKernelGGL(fn, g, dim3(kPairWaves * kWave), lds, stream, a);
-  return hipGetLastError();
-}
-
-// The gate/up pair from 17 rows, measured at [14336, 4096] (µs, graph back to
-// back; 16-row passes / 8-row halves / 16-row tiles): fp16 B = 17 74.1 /
-// 43.5 / 52.0, B = 32 76.2 / 44.3 / 54.4; e4m3 B = 17 40.5 / 43.6 / 29.4,
-// B = 32 42.4 / 45.3 / 32.2.  The halves read whole 128-byte lines; the
-// tiles read half lines but need a quarter of the accumulators, which e4m3
-// (whose halves kernel shuffles accumulators between MFMAs) gains from and
-// fp16 does not.  8-wave tile workgroups measured 5-6 us slower.
-static hipError_t launch_gemv_mfma_pair(const MfmaArgs& a0, bool fp8, int cu_count,
-                                        hipStream_t stream) {
-  const int tiles = tuning().gemv_pair_tiles;
-  if (tiles == 2 || (tiles == 0 && fp8)) return launch_gemv_mfma_tile16(a0, fp8, cu_count, stream);
-  MfmaArgs a = a0;
-  // The kernel's 32-bit weight offsets (see gemv_mfma_long_kernel).
-  if (a.N % kRowsPerGroup != 0 || (size_t)a.N * a.K * (fp8 ? 1 : 2) >= ((size_t)1 << 32))
-    return hipErrorInvalidValue;
-  const int bt = a.B <= 16 ? 2 : 4;  // passes of 16 or 32 rows
-  int kc = tuning().gemv_long_kc;
-  if (kc == 0 || kc > 2) kc = fp8 ? 2 : 1;
-  if (fp8) kc = 2;
-  const bool xs = kc == 2 && tuning().gemv_long_stage == 2;
-  int gpw = tuning().gemv_long_gpw;
-  if (gpw == 0) {
-    gpw = 7;
-    for (int g : {1, 2, 4})
-      if ((a.groups + g - 1) / g <= cu_count) {
-        gpw = g;
-        break;
-      }
-  }
-  a.gpw = gpw;
-  const int grid = (a.groups + gpw - 1) / gpw;
-  bool xs_eff = xs;
-  if (!fp8 && kc == 2 && bt == 4 && gpw == 7) {
-    kc = 1;  // as pick_pair_gpw substitutes
-    xs_eff = false;
-  }
-  const MfmaFn fn = fp8 ? pick_pair<true>(kc, bt, gpw, xs) : pick_pair<false>(kc, bt, gpw, xs);
-  const size_t lds = (xs_eff ? (size_t)kPairWaves * bt * kc * kWave * 16 : 0) +
-                     sizeof(float) * gpw * 2 * kPairWaves * 8 * bt * kRowsPerGroup;
-  if (lds > 48 * 1024) {
-    hipError_t e = allow_large_lds(reinterpret_cast<const void*>(fn), lds);
-    if (e != hipSuccess) return e;
-  }
-  dim3 g(grid, (a.B + 8 * bt - 1) / (8 * bt));
   hipLaunchKernelGGL(fn, g, dim3(kPairWaves * kWave), lds, stream, a);
   return hipGetLastError();
 }

@@ -204,13 +204,13 @@ int db_stream_read(const void* src, size_t bytes, int kb_per_wave, unsigned magi
  * 32 threads per merge workgroup: 1, 2, 4 or 8; 0 automatic), "f4_depth"
  * (tiles in flight per wave of the 8-wave whole-line F4 kernel: 1 or 2; 0
  * automatic), "gemv_long_kc" (k-steps of 32 columns per chunk of the
- * streamed-activation MFMA GEMV: 1, 2 or 4; 0 automatic), "gemv_long_gpw"
- * (its 8-row groups per workgroup: 1, 2, 4 or 7; 0 automatic),
- * "gemv_long_stage" (its activations: 1 loaded as B operands, 2 staged
- * through LDS; 0 automatic), "gemv_pair_min_batch" (batch rows from which
- * the gate/up pair streams its activations; 0 automatic, 17) and
- * "gemv_pair_tiles" (that pair's MFMA tiles: 1 two half-slices of 8 rows,
- * 2 16 rows; 0 automatic).
+ * MFMA GEMVs that stream their activations -- plain rows longer than 4096
+ * and the gate/up pair from 17 batch rows: 2 or 4; 0 automatic),
+ * "gemv_long_gpw" (8-row groups per workgroup of the long-row kernel: 1, 2
+ * or 4; 0 automatic), "gemv_long_stage" (its activations: 1 loaded as B
+ * operands, 2 staged through LDS; 0 automatic) and "gemv_pair_min_batch"
+ * (batch rows from which the gate/up pair streams its activations; 0
+ * automatic, 17).
  * Process-wide; no counterpart in the reference. */
 int db_tune(const char* key, int value);
 
