@@ -678,7 +678,7 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_long_kernel(MfmaArgs a) {
 // 32 rows that would be 7 groups x 2 matrices x 4 tiles of accumulators
 // (224 registers) on a CU's 56 rows; a version built that way had the
 // register allocator move accumulators through a shared temporary between
-// MFMAs and ran 1.5x slower (e4m3).  Here an MFMA
+// MFMAs and ran 1.6x slower (e4m3).  Here an MFMA
 // takes 16 weight rows (two of the workgroup's 8-row groups) against 16
 // batch rows over the same 32 columns, and every element of D is an output:
 // A row m = row m & 7 of group 2j + (m >> 3), k-group g4 = columns
@@ -698,6 +698,9 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_long_kernel(MfmaArgs a) {
 // groups; a last tile with one group duplicates it in rows 8..15, which are
 // not stored.  Launched with N a multiple of 8 and 2 N K bytes below 4 GiB
 // (32-bit lane offsets; every row of a live group below N).
+// NORM (RMSNorm -> gate/up, K <= 4096): before the stream each wave sums x^2
+// over its slice for every batch row of the pass; each streamed x chunk is
+// then normalised as fp16(fp16(x * inv_rms) * gamma).
 __device__ __forceinline__ u4 tile_half0(const u4& g0, const u4& g1) {
   u4 t;
 #pragma unroll
@@ -715,7 +718,7 @@ __device__ __forceinline__ u4 tile_half1(const u4& g0, const u4& g1) {
   return t;
 }
 
-template <int NWM, int WV, int KC, int BT16, int T, bool FP8>
+template <int NWM, int WV, int KC, int BT16, int T, bool FP8, bool NORM>
 __global__ __launch_bounds__(WV * kWave) void gemv_mfma_tile16_kernel(MfmaArgs a) {
   constexpr int kThreads = WV * kWave;
   constexpr int kStepsPerLoad = FP8 ? 2 : 1;  // k-steps in a 16-byte A operand
@@ -763,7 +766,9 @@ __global__ __launch_bounds__(WV * kWave) void gemv_mfma_tile16_kernel(MfmaArgs a
   auto wcol = [](int p) { return (FP8 ? 128 : 64) * p; };
   auto xcol = [](int t) { return FP8 ? 64 * (t >> 1) + 8 * (t & 1) : 32 * t; };
 
-  auto load = [&](u4 (&xs)[kXL], u4 (&ws)[NG][NWM][KWC], int c) {
+  // NORM: gamma at the activations' columns, loaded with each chunk.
+  constexpr int kGL = NORM ? KC : 1;
+  auto load = [&](u4 (&xs)[kXL], u4 (&gs)[kGL], u4 (&ws)[NG][NWM][KWC], int c) {
     const int c0 = 32 * KC * c;
 #pragma unroll
     for (int j = 0; j < NG; ++j) {
@@ -777,6 +782,10 @@ __global__ __launch_bounds__(WV * kWave) void gemv_mfma_tile16_kernel(MfmaArgs a
     }
 #pragma unroll
     for (int i = 0; i < kXL; ++i) xs[i] = ld16(xp[i / KC] + c0 + xcol(i % KC));
+    if constexpr (NORM) {
+#pragma unroll
+      for (int t = 0; t < KC; ++t) gs[t] = ld16(a.gamma + xcol0 + c0 + xcol(t));
+    }
   };
   f4 acc[T][NWM][BT16];
 #pragma unroll
@@ -798,7 +807,13 @@ __global__ __launch_bounds__(WV * kWave) void gemv_mfma_tile16_kernel(MfmaArgs a
             __builtin_bit_cast(h8, av[s]), __builtin_bit_cast(h8, xs[bt * KC + t0 + s]),
             acc[j][m][bt], 0, 0, 0);
   };
-  auto consume = [&](const u4 (&xs)[kXL], const u4 (&ws)[NG][NWM][KWC]) {
+  float inv[BT16];  // NORM: 1 / rms of this lane's batch rows
+  auto consume = [&](const u4 (&xl)[kXL], const u4 (&gs)[kGL], const u4 (&ws)[NG][NWM][KWC]) {
+    // NORM: fp16(fp16(x * inv_rms) * gamma), the torch stage's rounding
+    // points (see norm_mul).
+    u4 xs[kXL];
+#pragma unroll
+    for (int i = 0; i < kXL; ++i) xs[i] = NORM ? norm_mul(xl[i], gs[i % KC], inv[i / KC]) : xl[i];
 #pragma unroll
     for (int p = 0; p < KWC; ++p)
 #pragma unroll
@@ -812,18 +827,50 @@ __global__ __launch_bounds__(WV * kWave) void gemv_mfma_tile16_kernel(MfmaArgs a
         }
   };
 
-  u4 xa[kXL], wa[NG][NWM][KWC], xb[kXL], wb[NG][NWM][KWC];
-  load(xa, wa, 0);
+  u4 xa[kXL], ga[kGL], wa[NG][NWM][KWC], xb[kXL], gb[kGL], wb[NG][NWM][KWC];
+  load(xa, ga, wa, 0);  // in flight during the statistic below
+  if constexpr (NORM) {
+    // x^2 over this wave's K slice for every batch row of the pass, 8 rows
+    // at a time (lane l takes 16-byte pieces l and l + 64 of a row's slice,
+    // which covers K <= 4096), then over the waves in LDS.
+    __shared__ float red[WV][kPass];
+    const int pieces = slice / 8;
+    const u4 zero4 = {0, 0, 0, 0};
+    for (int r0 = 0; r0 < nb; r0 += 8) {
+      u4 v[8][2];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const _Float16* xr = a.x + (size_t)(b0 + min(r0 + i, nb - 1)) * a.K + sbase;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          v[i][h] = lane + 64 * h < pieces ? ld16(xr + 8 * (lane + 64 * h)) : zero4;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float ss = wave_sum(dot8(v[i][1], v[i][1], dot8(v[i][0], v[i][0], 0.0f)));
+        if (lane == 0 && r0 + i < nb) red[wave][r0 + i] = ss;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int bt = 0; bt < BT16; ++bt) {
+      const int r = min(16 * bt + c16, nb - 1);
+      float tot = 0.0f;
+#pragma unroll
+      for (int w = 0; w < WV; ++w) tot += red[w][r];
+      inv[bt] = 1.0f / sqrtf(tot / (float)a.K + a.eps);
+    }
+  }
   int c = 0;
   for (; c + 3 <= nch; c += 2) {
-    load(xb, wb, c + 1);
-    consume(xa, wa);
-    load(xa, wa, c + 2);
-    consume(xb, wb);
+    load(xb, gb, wb, c + 1);
+    consume(xa, ga, wa);
+    load(xa, ga, wa, c + 2);
+    consume(xb, gb, wb);
   }
-  if (c + 1 < nch) load(xb, wb, c + 1);
-  consume(xa, wa);
-  if (c + 1 < nch) consume(xb, wb);
+  if (c + 1 < nch) load(xb, gb, wb, c + 1);
+  consume(xa, ga, wa);
+  if (c + 1 < nch) consume(xb, gb, wb);
 
   // D[4 g4 + i][c16] = tile row 4 g4 + i (group 2j + (g4 >> 1), row
   // 4 (g4 & 1) + i) against batch row 16 bt + c16.
@@ -949,19 +996,31 @@ MfmaFn pick_long(int kc, int bt, int gpw, bool xs) {
 // or 4 tiles (2, 4 or 8 groups).
 constexpr int kPairWaves = 4;
 
-template <int KC, int BT16, bool FP8>
+template <int KC, int BT16, bool FP8, bool NORM>
 MfmaFn pick_pair_t(int t) {
-  return t == 1 ? gemv_mfma_tile16_kernel<2, kPairWaves, KC, BT16, 1, FP8>
-         : t == 2 ? gemv_mfma_tile16_kernel<2, kPairWaves, KC, BT16, 2, FP8>
-                  : gemv_mfma_tile16_kernel<2, kPairWaves, KC, BT16, 4, FP8>;
+  return t == 1 ? gemv_mfma_tile16_kernel<2, kPairWaves, KC, BT16, 1, FP8, NORM>
+         : t == 2 ? gemv_mfma_tile16_kernel<2, kPairWaves, KC, BT16, 2, FP8, NORM>
+                  : gemv_mfma_tile16_kernel<2, kPairWaves, KC, BT16, 4, FP8, NORM>;
+}
+
+// fp16 with the norm takes 2-k-step chunks only (4 would spill at 32 rows).
+template <bool FP8, bool NORM>
+MfmaFn pick_pair_n(int kc, int bt16, int t) {
+  if constexpr (!FP8 && NORM) {
+    (void)kc;
+    return bt16 == 1 ? pick_pair_t<2, 1, FP8, NORM>(t) : pick_pair_t<2, 2, FP8, NORM>(t);
+  } else {
+    if constexpr (!FP8) {
+      if (kc == 2)
+        return bt16 == 1 ? pick_pair_t<2, 1, FP8, NORM>(t) : pick_pair_t<2, 2, FP8, NORM>(t);
+    }
+    return bt16 == 1 ? pick_pair_t<4, 1, FP8, NORM>(t) : pick_pair_t<4, 2, FP8, NORM>(t);
+  }
 }
 
 template <bool FP8>
-MfmaFn pick_pair(int kc, int bt16, int t) {
-  if constexpr (!FP8) {
-    if (kc == 2) return bt16 == 1 ? pick_pair_t<2, 1, FP8>(t) : pick_pair_t<2, 2, FP8>(t);
-  }
-  return bt16 == 1 ? pick_pair_t<4, 1, FP8>(t) : pick_pair_t<4, 2, FP8>(t);
+MfmaFn pick_pair(int kc, int bt16, int t, bool norm) {
+  return norm ? pick_pair_n<FP8, true>(kc, bt16, t) : pick_pair_n<FP8, false>(kc, bt16, t);
 }
 
 }  // namespace
@@ -976,7 +1035,9 @@ static bool long_rows(GemvMode mode, int K) {
 // streams, one pass up to 32 rows.
 static bool pair_rows(GemvMode mode, int B, int K, int N) {
   const int pair_min = tuning().gemv_pair_min_batch > 0 ? tuning().gemv_pair_min_batch : 17;
-  return mode == kGemvSwiGLU && K % 2048 == 0 && N % kRowsPerGroup == 0 &&
+  // The RMSNorm mode's statistic pass covers K <= 4096 (2 pieces per lane).
+  const bool mode_ok = mode == kGemvSwiGLU || (mode == kGemvRmsNormSwiGLU && K <= 4096);
+  return mode_ok && K % 2048 == 0 && N % kRowsPerGroup == 0 &&
          (size_t)2 * N * K * 2 < ((size_t)1 << 32) && B >= pair_min;
 }
 
@@ -1034,7 +1095,7 @@ static hipError_t launch_gemv_mfma_long(const MfmaArgs& a0, bool fp8, int cu_cou
 // through a shared temporary between MFMAs); the direct tiles read half
 // lines.  4-k-step fp16 chunks measured 1.5-2.3 us slower, 8-wave
 // workgroups 5-6 us slower.
-static hipError_t launch_gemv_mfma_pair(const MfmaArgs& a0, bool fp8, int cu_count,
+static hipError_t launch_gemv_mfma_pair(const MfmaArgs& a0, bool norm, bool fp8, int cu_count,
                                         hipStream_t stream) {
   MfmaArgs a = a0;
   // The kernel's 32-bit lane offsets (see gemv_mfma_tile16_kernel).
@@ -1042,13 +1103,14 @@ static hipError_t launch_gemv_mfma_pair(const MfmaArgs& a0, bool fp8, int cu_cou
       (size_t)2 * a.N * a.K * (fp8 ? 1 : 2) >= ((size_t)1 << 32))
     return hipErrorInvalidValue;
   const int bt16 = a.B <= 16 ? 1 : 2;  // passes of 16 or 32 rows
-  const int kc = fp8 || tuning().gemv_long_kc == 4 ? 4 : 2;
+  const int kc = fp8 ? 4 : !norm && tuning().gemv_long_kc == 4 ? 4 : 2;
   int gpw = (a.groups + cu_count - 1) / cu_count;
   if (gpw > 8) gpw = 8;
   const int t = gpw <= 2 ? 1 : gpw <= 4 ? 2 : 4;
   a.gpw = gpw;
   const int grid = (a.groups + gpw - 1) / gpw;
-  const MfmaFn fn = fp8 ? pick_pair<true>(kc, bt16, t) : pick_pair<false>(kc, bt16, t);
+  const MfmaFn fn =
+      fp8 ? pick_pair<true>(kc, bt16, t, norm) : pick_pair<false>(kc, bt16, t, norm);
   const size_t lds = sizeof(float) * 2 * t * 2 * kPairWaves * 16 * bt16 * kRowsPerGroup;
   if (lds > 48 * 1024) {
     hipError_t e = allow_large_lds(reinterpret_cast<const void*>(fn), lds);
@@ -1076,7 +1138,8 @@ hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
   a.eps = eps;
   a.groups = (N + kRowsPerGroup - 1) / kRowsPerGroup;
   if (long_rows(mode, K)) return launch_gemv_mfma_long(a, w.fp8, cu_count, stream);
-  if (pair_rows(mode, B, K, N)) return launch_gemv_mfma_pair(a, w.fp8, cu_count, stream);
+  if (pair_rows(mode, B, K, N))
+    return launch_gemv_mfma_pair(a, mode == kGemvRmsNormSwiGLU, w.fp8, cu_count, stream);
   int grid = min(a.groups, cu_count);
   a.gpw = (a.groups + grid - 1) / grid;
   if (a.gpw > kMaxGroupsPerWg) a.gpw = kMaxGroupsPerWg;

@@ -265,64 +265,84 @@ def test_long_row_gemv_launch_shapes_agree():
 
 
 # --------------------------------------------------- gate/up pair, streamed x
-# The gate/up pair + SwiGLU from 17 rows (K a multiple of 2048, N of 8)
-# streams x in K chunks on 4-wave workgroups: 32 rows per pass, the full
-# config-2 shape at B=32 (7 groups per workgroup), a second pass above 32,
-# fewer groups than CUs, fp16 and e4m3; N not a multiple of 8 keeps the
-# 16-row passes.
+# The gate/up pair + SwiGLU, and RMSNorm -> gate/up + SwiGLU, from 17 rows
+# (K a multiple of 2048, N of 8; K <= 4096 with the norm) streams x in K
+# chunks on 4-wave workgroups: 32 rows per pass, the full config-2 shape at
+# B=32 (7 groups per workgroup), a second pass above 32, fewer groups than
+# CUs, fp16 and e4m3; N not a multiple of 8 keeps the 16-row passes.
 PAIR_CASES = [
-    ("f16", 32, 4096, 14336), ("f16", 17, 4096, 2048), ("f16", 40, 2048, 776),
-    ("f16", 24, 4096, 1001), ("f16", 33, 6144, 264),
-    ("fp8", 32, 4096, 14336), ("fp8", 20, 2048, 1792), ("fp8", 48, 4096, 520),
+    ("f2", "f16", 32, 4096, 14336), ("f2", "f16", 17, 4096, 2048), ("f2", "f16", 40, 2048, 776),
+    ("f2", "f16", 24, 4096, 1001), ("f2", "f16", 33, 6144, 264),
+    ("f2", "fp8", 32, 4096, 14336), ("f2", "fp8", 20, 2048, 1792), ("f2", "fp8", 48, 4096, 520),
+    ("f2n", "f16", 32, 4096, 14336), ("f2n", "f16", 17, 2048, 1000), ("f2n", "f16", 40, 4096, 264),
+    ("f2n", "fp8", 24, 4096, 14336), ("f2n", "fp8", 33, 2048, 776),
 ]
 
 
-@pytest.mark.parametrize("dtype,B,K,N", PAIR_CASES)
-def test_gateup_pair_streamed_parity(dtype, B, K, N):
+@pytest.mark.parametrize("mode,dtype,B,K,N", PAIR_CASES)
+def test_gateup_pair_streamed_parity(mode, dtype, B, K, N):
     from decodebench_amd.quant import quantize_e4m3_rows
 
-    print(f"[pair] {dtype} B={B} K={K} N={N}", flush=True)
+    print(f"[pair] {mode} {dtype} B={B} K={K} N={N}", flush=True)
     gen = torch.Generator().manual_seed(9000 + B + K + N)
     x = randn(gen, (B, K))
+    g = randn(gen, (K,), std=0.1, mean=1.0)
     Wg = randn(gen, (N, K), std=0.02)
     Wu = randn(gen, (N, K), std=0.02)
+    norm = mode == "f2n"
+    xin = stages.rmsnorm(x, g, 1e-6) if norm else x
+    xin_np = cref.rmsnorm(x.numpy(), g.numpy(), 1e-6) if norm else x.numpy()
     if dtype == "fp8":
         Gq, sg = quantize_e4m3_rows(Wg)
         Uq, su = quantize_e4m3_rows(Wu)
-        y = ops.f2_gateup_swiglu(x.cuda(), Gq.cuda(), Uq.cuda(), sg.cuda(), su.cuda())
-        ref = stages.f2_fp8(x, Gq, sg, Uq, su)
-        exact = cref.f2_fp8_exact(x.numpy(), Gq.view(torch.uint8).numpy(), sg.numpy(),
+        if norm:
+            y = ops.f2_rmsnorm_gateup_swiglu(x.cuda(), g.cuda(), Gq.cuda(), Uq.cuda(),
+                                             sg=sg.cuda(), su=su.cuda(), eps=1e-6)
+        else:
+            y = ops.f2_gateup_swiglu(x.cuda(), Gq.cuda(), Uq.cuda(), sg.cuda(), su.cuda())
+        ref = stages.f2_fp8(xin, Gq, sg, Uq, su)
+        exact = cref.f2_fp8_exact(xin_np, Gq.view(torch.uint8).numpy(), sg.numpy(),
                                   Uq.view(torch.uint8).numpy(), su.numpy())
     else:
-        y = ops.f2_gateup_swiglu(x.cuda(), Wg.cuda(), Wu.cuda())
-        ref, exact = stages.f2(x, Wg, Wu), cref.f2_exact(x.numpy(), Wg.numpy(), Wu.numpy())
+        if norm:
+            y = ops.f2_rmsnorm_gateup_swiglu(x.cuda(), g.cuda(), Wg.cuda(), Wu.cuda(), eps=1e-6)
+        else:
+            y = ops.f2_gateup_swiglu(x.cuda(), Wg.cuda(), Wu.cuda())
+        ref, exact = stages.f2(xin, Wg, Wu), cref.f2_exact(xin_np, Wg.numpy(), Wu.numpy())
     torch.cuda.synchronize()
     assert y.shape == (B, N)
-    assert_parity(y, ref, exact, 5e-3, f"pair {dtype} B={B} K={K} N={N}")
+    assert_parity(y, ref, exact, 5e-3, f"pair {mode} {dtype} B={B} K={K} N={N}")
 
 
 def test_gateup_pair_launch_shapes_agree():
-    """The config-2 gate/up pair at 16 and 32 rows through the streamed
-    16-row-tile kernel (2- and 4-k-step chunks) and through the 16-row passes
-    agrees to fp32 summation order, fp16 and e4m3."""
+    """The config-2 gate/up pair, with and without the fused RMSNorm, at 16 and
+    32 rows through the streamed 16-row-tile kernel (2- and 4-k-step chunks)
+    and through the 16-row passes agrees to fp32 summation order, fp16 and
+    e4m3."""
     from decodebench_amd.quant import quantize_e4m3_rows
 
     gen = torch.Generator().manual_seed(80)
     lib = ops.load_library()
     Wg = randn(gen, (14336, 4096), std=0.02)
     Wu = randn(gen, (14336, 4096), std=0.02)
+    g = randn(gen, (4096,), std=0.1, mean=1.0).cuda()
     Gq, sg = (t.cuda() for t in quantize_e4m3_rows(Wg))
     Uq, su = (t.cuda() for t in quantize_e4m3_rows(Wu))
     Wg, Wu = Wg.cuda(), Wu.cuda()
     try:
         for B in (16, 32):
             x = randn(gen, (B, 4096)).cuda()
+            def calls():
+                return (ops.f2_gateup_swiglu(x, Wg, Wu), ops.f2_gateup_swiglu(x, Gq, Uq, sg, su),
+                        ops.f2_rmsnorm_gateup_swiglu(x, g, Wg, Wu),
+                        ops.f2_rmsnorm_gateup_swiglu(x, g, Gq, Uq, sg=sg, su=su))
+
             assert lib.db_tune(b"gemv_pair_min_batch", 1 << 20) == 0
-            base = (ops.f2_gateup_swiglu(x, Wg, Wu), ops.f2_gateup_swiglu(x, Gq, Uq, sg, su))
+            base = calls()
             assert lib.db_tune(b"gemv_pair_min_batch", 2) == 0
             for kc in (2, 4):
                 assert lib.db_tune(b"gemv_long_kc", kc) == 0
-                got = (ops.f2_gateup_swiglu(x, Wg, Wu), ops.f2_gateup_swiglu(x, Gq, Uq, sg, su))
+                got = calls()
                 for a, b in zip(got, base):
                     err = rel_l2(a.float().cpu().numpy(), b.float().cpu().numpy())
                     assert err < 1e-3, f"B={B} kc={kc}: rel-L2 {err:.2e}"
