@@ -276,6 +276,8 @@ PAIR_CASES = [
     ("f2", "fp8", 32, 4096, 14336), ("f2", "fp8", 20, 2048, 1792), ("f2", "fp8", 48, 4096, 520),
     ("f2n", "f16", 32, 4096, 14336), ("f2n", "f16", 17, 2048, 1000), ("f2n", "f16", 40, 4096, 264),
     ("f2n", "fp8", 24, 4096, 14336), ("f2n", "fp8", 33, 2048, 776),
+    # one group (a tile whose second half repeats it) and two groups
+    ("f2", "f16", 17, 2048, 8), ("f2n", "fp8", 32, 4096, 16),
 ]
 
 
