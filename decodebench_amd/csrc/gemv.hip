@@ -158,10 +158,13 @@ hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
   // activation prologue once.  Measured on MI355X (graph back-to-back):
   // F1-QKV 9.2 -> 9.05 us; with up to 32 waves per CU the 768 workgroups of
   // 8 rows run in two rounds (two resident per CU at 91 VGPRs) and some CUs
-  // take a fourth.  The plain projection keeps the default (the fp16 decode
-  // layer measured 0.1-0.5 us slower with it).
-  const bool f1_persistent = mode == kGemvRmsNorm && !w.fp8 && nb == 1 && R == 1 &&
-                             wv == 8 && tuning().gemv_waves_per_cu <= 0;
+  // take a fourth.  e4m3 F1 (4-wave workgroups of 2 rows) takes one
+  // workgroup per CU the same way: F1-QKV 6.07-6.11 -> 5.75-5.79 us, F1
+  // 4.67 -> 4.58-4.61 us.  The plain projection keeps the default (the fp16
+  // decode layer measured 0.1-0.5 us slower with it).
+  const bool f1_persistent = mode == kGemvRmsNorm && nb == 1 &&
+                             (w.fp8 || (R == 1 && wv == 8)) &&
+                             tuning().gemv_waves_per_cu <= 0;
   const int waves = f1_persistent ? waves_for(a.groups, cu_count * wv)
                                   : pick_waves(a.groups, cu_count);
   dim3 grid((waves + wv - 1) / wv, (B + nb - 1) / nb);
