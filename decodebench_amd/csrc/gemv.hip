@@ -161,12 +161,17 @@ hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
   // take a fourth.  e4m3 F1 (4-wave workgroups of 2 rows) takes one
   // workgroup per CU the same way: F1-QKV 6.07-6.11 -> 5.75-5.79 us, F1
   // 4.67 -> 4.58-4.61 us.  The plain projection keeps the default (the fp16
-  // decode layer measured 0.1-0.5 us slower with it).
-  const bool f1_persistent = mode == kGemvRmsNorm && nb == 1 &&
-                             (w.fp8 || (R == 1 && wv == 8)) &&
-                             tuning().gemv_waves_per_cu <= 0;
-  const int waves = f1_persistent ? waves_for(a.groups, cu_count * wv)
-                                  : pick_waves(a.groups, cu_count);
+  // decode layer measured 0.1-0.5 us slower with it), except the e4m3 rows
+  // longer than 4096, whose 8-wave workgroups of one row per wave gain from
+  // it (down projection [4096, 14336] 11.08-11.12 -> 10.73-10.79 us; a sweep
+  // of 1-16 workgroups' worth of waves per CU found nothing better for the
+  // fp16 projections or RMSNorm -> gate/up).
+  const bool persistent = ((mode == kGemvRmsNorm && nb == 1 &&
+                            (w.fp8 || (R == 1 && wv == 8))) ||
+                           fp8_long_rows) &&
+                          tuning().gemv_waves_per_cu <= 0;
+  const int waves = persistent ? waves_for(a.groups, cu_count * wv)
+                               : pick_waves(a.groups, cu_count);
   dim3 grid((waves + wv - 1) / wv, (B + nb - 1) / nb);
   hipLaunchKernelGGL(fn, grid, dim3(wv * kWave), lds, stream, a);
   return hipGetLastError();
