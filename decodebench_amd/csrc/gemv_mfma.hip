@@ -1,4 +1,7 @@
-// gemv_mfma.hip -- batched decode GEMV on MFMA (batch 2..16 per pass) for gfx950.
+// gemv_mfma.hip -- batched decode GEMV on MFMA for gfx950: gemv_mfma_kernel
+// (passes of 16 or 32 batch rows), and the kernels that also stream the
+// activations, gemv_mfma_long_kernel (rows longer than 4096) and
+// gemv_mfma_tile16_kernel (the gate/up pair above 16 rows).
 //
 // y[B,N] = op(x[B,K]) . W^T for the four GEMV modes of gemv.hip (plain,
 // RMSNorm-fused F1, gate/up + SwiGLU F2, RMSNorm -> gate/up + SwiGLU) with
@@ -37,8 +40,9 @@
 // weight matrix takes 32-row passes when the LDS holds rows 16..31 of x next
 // to the partial sums (XB), otherwise passes are 16 rows.
 // Plain GEMV with longer rows (K a multiple of 2048 above 4096, the down
-// projection) and the gate/up pair above 16 rows take kernels that stream x
-// as well: gemv_mfma_long_kernel and gemv_mfma_tile16_kernel.
+// projection) and the gate/up pair above 16 rows, with or without the
+// RMSNorm, take kernels that stream x as well: gemv_mfma_long_kernel and
+// gemv_mfma_tile16_kernel (below).
 #include "gemv_valu.h"
 
 namespace dbk {
