@@ -860,6 +860,47 @@ def test_decode_layer_replays_correctly_in_a_graph(dtype):
         assert torch.equal(out, eager), f"{dtype} replay {i} differs from eager"
 
 
+def test_streamed_gemv_kernels_replay_correctly_in_a_graph():
+    """The kernels that stream their activations (the gate/up pair with and
+    without the RMSNorm above 16 rows, the long-row down projection) captured
+    in one hipGraph replay bit-identically to eager, with eager work between
+    replays."""
+    from decodebench_amd.quant import quantize_e4m3_rows
+
+    gen = torch.Generator().manual_seed(12)
+    x32 = randn(gen, (32, 4096)).cuda()
+    x24 = randn(gen, (24, 4096)).cuda()
+    x16 = randn(gen, (16, 14336)).cuda()
+    g = randn(gen, (4096,), std=0.1, mean=1.0).cuda()
+    Wg = randn(gen, (14336, 4096), std=0.02)
+    Wu = randn(gen, (14336, 4096), std=0.02)
+    Gq, sg = (t.cuda() for t in quantize_e4m3_rows(Wg))
+    Uq, su = (t.cuda() for t in quantize_e4m3_rows(Wu))
+    Wg, Wu = Wg.cuda(), Wu.cuda()
+    Wd = randn(gen, (4096, 14336), std=1.0 / 128).cuda()
+
+    def body():
+        return (ops.f2_gateup_swiglu(x32, Wg, Wu),
+                ops.f2_rmsnorm_gateup_swiglu(x24, g, Gq, Uq, sg=sg, su=su),
+                ops.gemv(x16, Wd))
+
+    eager = [t.clone() for t in body()]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        body()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = body()
+    for i in range(5):
+        x32.add_(0.0)                    # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        for e, o in zip(eager, outs):
+            assert torch.equal(e, o), f"replay {i} differs from eager"
+
+
 def test_ops_replay_correctly_in_a_graph():
     gen = torch.Generator().manual_seed(11)
     x = randn(gen, (1, 4096)).cuda()
