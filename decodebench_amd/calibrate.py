@@ -122,7 +122,8 @@ def _graph_us(fn, args: list, min_launches: int = 48, replays: int = 10) -> floa
     with torch.cuda.graph(graph):
         for i in range(per_graph):
             fn(args[i % n])
-    graph.replay()
+    for _ in range(3):  # warm-up replays: the first after capture runs slower
+        graph.replay()
     torch.cuda.synchronize()
     e0, e1 = _events()
     samples = []
@@ -229,7 +230,7 @@ FLOOR_SIZES = (4_210_688, 16_818_176, 33_579_008, 33_570_816, 50_360_320, 134_23
 
 @dataclass
 class StreamFloor:
-    rows: list            # (bytes, {kb_per_wave: us}) per size
+    rows: list            # (bytes, {(kb_per_wave, waves_per_workgroup): us}) per size
     replicas: dict        # bytes -> replicas rotated through
     fit_us: float         # fixed cost a of t = a + bytes / bw over the best time per size
     fit_gbs: float        # bw
@@ -238,28 +239,33 @@ class StreamFloor:
         return min(dict(self.rows)[nbytes].values())
 
     def render(self) -> str:
-        kbs = sorted(self.rows[0][1])
-        head = " | ".join(f"{k} KB/wave us" for k in kbs)
+        shapes = list(self.rows[0][1])
+        head = " | ".join(f"{kb} KB x{wv} us" for kb, wv in shapes)
         out = [f"| bytes | {head} | best GB/s | % of 8 TB/s | 70% bar us | replicas |",
-               "|---|" + "---|" * (len(kbs) + 4)]
+               "|---|" + "---|" * (len(shapes) + 4)]
         for nbytes, per in self.rows:
             best = min(per.values())
             gbs = nbytes / (best * 1e3)
-            out.append(f"| {nbytes:,} | " + " | ".join(f"{per[k]:.2f}" for k in kbs) +
+            out.append(f"| {nbytes:,} | " + " | ".join(f"{per[s]:.2f}" for s in shapes) +
                        f" | {gbs:.0f} | {gbs / 80:.1f} | {nbytes / 8e12 / 0.7 * 1e6:.2f} | "
                        f"{self.replicas[nbytes]} |")
         out.append(f"floor fit: t = {self.fit_us:.2f} us + bytes / {self.fit_gbs:.0f} GB/s")
         return "\n".join(out)
 
 
-def stream_floor(sizes=FLOOR_SIZES, kbs=(4, 8, 16), min_launches: int = 96,
+# (KB per wave, waves per workgroup) of the streaming probe.
+FLOOR_SHAPES = ((4, 1), (4, 4), (8, 2), (8, 4), (16, 4))
+
+
+def stream_floor(sizes=FLOOR_SIZES, shapes=FLOOR_SHAPES, min_launches: int = 96,
                  replays: int = 10) -> StreamFloor:
     """Single-launch streaming floor: ``db_stream_read`` (a read-only kernel
-    of 16-byte non-temporal loads, each wave one contiguous chunk of
-    ``kb`` KB) timed back to back in a hipGraph over zero-filled buffers
-    rotated through a working set of at least 2 x (8 x 4 MB L2 + 256 MB
-    Infinity Cache), for each byte count in ``sizes``.  A fused kernel that
-    reads the same bytes in one launch cannot beat the best of these."""
+    of 16-byte non-temporal loads, each wave one contiguous chunk of ``kb``
+    KB, workgroups of 1, 2 or 4 waves) timed back to back in a hipGraph over
+    zero-filled buffers rotated through a working set of at least
+    2 x (8 x 4 MB L2 + 256 MB Infinity Cache), for each byte count in
+    ``sizes``.  A fused kernel that reads the same bytes in one launch
+    cannot beat the best of these."""
     import torch
 
     from decodebench_amd import ops
@@ -269,20 +275,24 @@ def stream_floor(sizes=FLOOR_SIZES, kbs=(4, 8, 16), min_launches: int = 96,
     working_set = 2 * (8 * 4 + 256) * 2**20
     rows, reps = [], {}
     sink = None
-    for nbytes in sizes:
-        padded = -(-nbytes // chunk) * chunk
-        n = max(2, -(-working_set // padded))
-        bufs = [torch.zeros(padded, dtype=torch.uint8, device="cuda") for _ in range(n)]
-        if sink is None or sink.numel() < padded // 16:
-            sink = torch.empty(padded // 16, dtype=torch.int32, device="cuda")
-        per = {}
-        for kb in kbs:
-            per[kb] = _graph_us(lambda b, kb=kb: ops.stream_read(b, kb, sink), bufs,
-                                min_launches=min_launches, replays=replays)
-        rows.append((nbytes, per))
-        reps[nbytes] = n
-        del bufs
-        torch.cuda.empty_cache()
+    try:
+        for nbytes in sizes:
+            padded = -(-nbytes // chunk) * chunk
+            n = max(2, -(-working_set // padded))
+            bufs = [torch.zeros(padded, dtype=torch.uint8, device="cuda") for _ in range(n)]
+            if sink is None or sink.numel() < padded // 16:
+                sink = torch.empty(padded // 16, dtype=torch.int32, device="cuda")
+            per = {}
+            for kb, wv in shapes:
+                ops.tune("stream_waves", wv)
+                per[(kb, wv)] = _graph_us(lambda b, kb=kb: ops.stream_read(b, kb, sink), bufs,
+                                          min_launches=min_launches, replays=replays)
+            rows.append((nbytes, per))
+            reps[nbytes] = n
+            del bufs
+            torch.cuda.empty_cache()
+    finally:
+        ops.tune("stream_waves", 0)
     xs = [nb for nb, _ in rows]
     ys = [min(per.values()) for _, per in rows]
     mx, my = sum(xs) / len(xs), sum(ys) / len(ys)

@@ -368,6 +368,10 @@ int db_tune(const char* key, int value) {
     if (value < 0 || value == 1)
       return fail(DB_ERR_INVALID, "db_tune: gemv_pair_min_batch must be 0 (automatic) or >= 2");
     t.gemv_pair_min_batch = value;
+  } else if (!strcmp(key, "stream_waves")) {
+    if (value != 0 && value != 1 && value != 2 && value != 4)
+      return fail(DB_ERR_INVALID, "db_tune: stream_waves must be 0, 1, 2 or 4");
+    t.stream_waves = value;
   } else if (!strcmp(key, "f4_min_tiles")) {
     if (value < 1) return fail(DB_ERR_INVALID, "db_tune: f4_min_tiles must be >= 1");
     t.f4_min_tiles = value;

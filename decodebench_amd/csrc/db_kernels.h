@@ -26,6 +26,7 @@ struct Tuning {
   int gemv_long_gpw = 0;       // long-row MFMA GEMV row groups per workgroup: 0 auto, 1, 2, 4
   int gemv_long_stage = 0;     // long-row MFMA GEMV x: 0 auto, 1 direct, 2 LDS-staged
   int gemv_pair_min_batch = 0; // gate/up pair rows from which x streams (0: 17)
+  int stream_waves = 0;        // db_stream_read waves per workgroup: 0 (4), 1, 2 or 4
 };
 Tuning& tuning();
 

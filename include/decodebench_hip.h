@@ -182,7 +182,8 @@ int db_null_kernel(void* stream);
  * moves vs its time) and as a read-only, known-size reference for the HBM
  * traffic counters.  Every wave reads one contiguous chunk of kb_per_wave KB
  * (4, 8 or 16) with 16-byte non-temporal loads, 1 KB per wave-wide load
- * instruction, all issued before any is used.  The loaded words are folded
+ * instruction, all issued before any is used; workgroups of 4 waves, or 1
+ * or 2 with db_tune("stream_waves", n).  The loaded words are folded
  * into one value per lane, stored to sink[] only if it equals `magic`
  * (choose a value that cannot occur, e.g. with src zero-filled and magic
  * non-zero), so the kernel reads `bytes` and writes nothing.
@@ -208,9 +209,10 @@ int db_stream_read(const void* src, size_t bytes, int kb_per_wave, unsigned magi
  * and the gate/up pair from 17 batch rows: 2 or 4; 0 automatic),
  * "gemv_long_gpw" (8-row groups per workgroup of the long-row kernel: 1, 2
  * or 4; 0 automatic), "gemv_long_stage" (its activations: 1 loaded as B
- * operands, 2 staged through LDS; 0 automatic) and "gemv_pair_min_batch"
+ * operands, 2 staged through LDS; 0 automatic), "gemv_pair_min_batch"
  * (batch rows from which the gate/up pair streams its activations; 0
- * automatic, 17).
+ * automatic, 17) and "stream_waves" (db_stream_read's waves per workgroup:
+ * 1, 2 or 4; 0 is 4).
  * Process-wide; no counterpart in the reference. */
 int db_tune(const char* key, int value);
 
