@@ -105,9 +105,6 @@ struct MfmaArgs {
 
 // KH: k-steps (32 columns each) per half slice, K / 512.
 // BT: batch column tiles of 8 (1 for batch <= 8, 2 for <= 16).
-// UPS: groups per register set.  When a workgroup's groups fit in one set
-// (UPS >= groups per workgroup) they are all requested before the prologue
-// and no loop runs; otherwise two sets alternate.
 // FP8: e4m3 weights.  A 16-byte load then holds 16 weights, the A operands
 // of two k-steps after v_cvt_scalef32_pk_f16_fp8 widening.  The activations
 // are loaded in the same column order, so the dot products are unchanged;
@@ -117,7 +114,7 @@ struct MfmaArgs {
 // (each wave its own, 16 KB x KH / 8 per wave) and read back per group, so
 // every weight tile feeds 32 rows instead of being re-read by a second
 // 16-row pass.
-template <int MODE, int KH, int BT, int UPS, bool SINGLE, bool FP8, bool XB>
+template <int MODE, int KH, int BT, bool FP8, bool XB>
 __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   constexpr int NWM = gemv_is_swiglu(MODE) ? 2 : 1;
   constexpr int KW = FP8 ? KH / 2 : KH;  // 16-byte weight loads per row and slice
@@ -173,23 +170,20 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
                                        (int)gridDim.x);
   const unsigned char* wmat[2] = {static_cast<const unsigned char*>(a.w0),
                                   static_cast<const unsigned char*>(a.w1)};
-  // `checked`: skip groups past my_groups (only outside the steady loop,
-  // whose loads are unconditional so the compiler waits per set).
-  auto load_set = [&](u4 (&dst)[UPS][NWM][KW], int j0, bool checked) {
+  // A register set holds one group.  `checked`: skip a group past
+  // my_groups (only outside the steady loop, whose loads are unconditional so
+  // the compiler waits per set).
+  auto load_set = [&](u4 (&dst)[NWM][KW], int j, bool checked) {
+    if (checked && j >= my_groups) return;
+    const int grp = blockIdx.x + gridDim.x * min(j, my_groups - 1);
+    const int row = min(grp * kRowsPerGroup + r8, a.N - 1);
 #pragma unroll
-    for (int q = 0; q < UPS; ++q) {
-      if (checked && j0 + q >= my_groups) break;
-      const int grp = blockIdx.x + gridDim.x * min(j0 + q, my_groups - 1);
-      const int row = min(grp * kRowsPerGroup + r8, a.N - 1);
+    for (int m = 0; m < NWM; ++m)
 #pragma unroll
-      for (int m = 0; m < NWM; ++m)
-#pragma unroll
-        for (int t = 0; t < KW; ++t)
-          dst[q][m][t] =
-              FP8 ? ld_stream(wmat[m] + (size_t)row * a.K + xcol(2 * t))
-                  : ld_stream(reinterpret_cast<const _Float16*>(wmat[m]) + (size_t)row * a.K +
-                              kcol + 64 * t);
-    }
+      for (int t = 0; t < KW; ++t)
+        dst[m][t] = FP8 ? ld_stream(wmat[m] + (size_t)row * a.K + xcol(2 * t))
+                        : ld_stream(reinterpret_cast<const _Float16*>(wmat[m]) +
+                                    (size_t)row * a.K + kcol + 64 * t);
   };
 
   // ---- activation slice -> registers (B operand) ------------------------
@@ -219,7 +213,7 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
     if constexpr (gemv_has_norm(MODE))
       gchunk = ld16(a.gamma + 8 * min((int)threadIdx.x, a.K / 8 - 1));
   };
-  u4 wa[UPS][NWM][KW];
+  u4 wa[NWM][KW];
   if constexpr (kStage) {
     constexpr int kSliceChunks = 8 * KH;                // 16-byte chunks of a row's slice
     constexpr int kRowsPerLoad = kWave / kSliceChunks;  // 1 (K = 4096) or 2 (K = 2048)
@@ -367,11 +361,9 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   }
 
   // ---- stream the groups ------------------------------------------------
-  auto consume = [&](const u4 (&src)[UPS][NWM][KW], int j0) {
-#pragma unroll
-    for (int q = 0; q < UPS; ++q) {
-      const int j = j0 + q;
-      if (j >= my_groups) break;
+  auto consume = [&](const u4 (&src)[NWM][KW], int j) {
+    if (j >= my_groups) return;
+    {
 #pragma unroll
       for (int m = 0; m < NWM; ++m) {
         // e4m3: the A operands of the KH k-steps, widened to fp16 once per
@@ -379,14 +371,14 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
         u4 av[FP8 ? KH : 1];
         if constexpr (FP8) {
 #pragma unroll
-          for (int t = 0; t < KW; ++t) e4m3x16_to_h(src[q][m][t], av[2 * t], av[2 * t + 1]);
+          for (int t = 0; t < KW; ++t) e4m3x16_to_h(src[m][t], av[2 * t], av[2 * t + 1]);
         }
 #pragma unroll
         for (int bt = 0; bt < BT; ++bt) {
           f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
           for (int t = 0; t < KH; ++t) {
-            const u4 at = FP8 ? av[FP8 ? t : 0] : src[q][m][FP8 ? 0 : t];
+            const u4 at = FP8 ? av[FP8 ? t : 0] : src[m][FP8 ? 0 : t];
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, at),
                                                          __builtin_bit_cast(h8, xr[bt][t]), acc,
                                                          0, 0, 0);
@@ -405,7 +397,7 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
             f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int t = 0; t < KH; ++t) {
-              const u4 at = FP8 ? av[FP8 ? t : 0] : src[q][m][FP8 ? 0 : t];
+              const u4 at = FP8 ? av[FP8 ? t : 0] : src[m][FP8 ? 0 : t];
               const u4 bx = xbuf[((wave * 2 + bt) * KH + t) * kWave + xslot(g4, half, r8, t)];
               acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, at),
                                                            __builtin_bit_cast(h8, bx), acc, 0, 0,
@@ -421,26 +413,24 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
     }
   };
 
-  if constexpr (SINGLE) {
-    consume(wa, 0);  // every group of the workgroup is in set A
-  } else {
+  {
     // Two register sets; the steady loop loads and consumes set B inside
     // one iteration (see flashdecode.hip for why that matters to the
     // compiler).
-    u4 wb[UPS][NWM][KW];
+    u4 wb[NWM][KW];
     int j = 0;
-    for (; j + 3 * UPS <= my_groups; j += 2 * UPS) {
-      load_set(wb, j + UPS, false);
+    for (; j + 3 <= my_groups; j += 2) {
+      load_set(wb, j + 1, false);
       consume(wa, j);
-      load_set(wa, j + 2 * UPS, false);
-      consume(wb, j + UPS);
+      load_set(wa, j + 2, false);
+      consume(wb, j + 1);
     }
-    // Fewer than 3 * UPS groups remain; set A holds the first UPS of them.
-    if (j + UPS < my_groups) load_set(wb, j + UPS, true);
+    // Fewer than 3 groups remain; set A holds the first of them.
+    if (j + 1 < my_groups) load_set(wb, j + 1, true);
     consume(wa, j);
-    if (j + 2 * UPS < my_groups) load_set(wa, j + 2 * UPS, true);
-    if (j + UPS < my_groups) consume(wb, j + UPS);
-    if (j + 2 * UPS < my_groups) consume(wa, j + 2 * UPS);
+    if (j + 2 < my_groups) load_set(wa, j + 2, true);
+    if (j + 1 < my_groups) consume(wb, j + 1);
+    if (j + 2 < my_groups) consume(wa, j + 2);
   }
 
   __syncthreads();
@@ -931,42 +921,35 @@ using MfmaFn = void (*)(MfmaArgs);
 // 10.9 us, fp16 B = 16 14.7-14.8 -> 14.3-14.6 us.  The more weight requests
 // all CUs have outstanding while x (which every workgroup reads) is still
 // on its way, the later x arrives.
-template <int MODE, int KH, int BT, bool FP8>
-MfmaFn pick_ups(int ups) {
-  (void)ups;
-  return gemv_mfma_kernel<MODE, KH, BT, 1, false, FP8, false>;
-}
-
 template <int MODE, int KH, bool FP8>
-MfmaFn pick_bt(int bt, int ups) {
-  return bt == 1 ? pick_ups<MODE, KH, 1, FP8>(ups) : pick_ups<MODE, KH, 2, FP8>(ups);
+MfmaFn pick_bt(int bt) {
+  return bt == 1 ? gemv_mfma_kernel<MODE, KH, 1, FP8, false>
+                 : gemv_mfma_kernel<MODE, KH, 2, FP8, false>;
 }
 
 template <int MODE, bool FP8>
-MfmaFn pick_kh(int kh, int bt, int ups) {
-  return kh == 4 ? pick_bt<MODE, 4, FP8>(bt, ups) : pick_bt<MODE, 8, FP8>(bt, ups);
+MfmaFn pick_kh(int kh, int bt) {
+  return kh == 4 ? pick_bt<MODE, 4, FP8>(bt) : pick_bt<MODE, 8, FP8>(bt);
 }
 
-// 32-row passes of one weight matrix (XB): one group per alternating set,
-// since both halves of the pass and set A are live at the normalisation.
+// 32-row passes of one weight matrix (XB).
 template <int MODE, bool FP8>
 MfmaFn pick_xb(int kh) {
-  return kh == 4 ? gemv_mfma_kernel<MODE, 4, 2, 1, false, FP8, true>
-                 : gemv_mfma_kernel<MODE, 8, 2, 1, false, FP8, true>;
+  return kh == 4 ? gemv_mfma_kernel<MODE, 4, 2, FP8, true>
+                 : gemv_mfma_kernel<MODE, 8, 2, FP8, true>;
 }
 
 template <bool FP8>
-MfmaFn pick_mode(GemvMode mode, int kh, int bt, int ups, bool xb) {
+MfmaFn pick_mode(GemvMode mode, int kh, int bt, bool xb) {
   if (xb) return mode == kGemvRmsNorm ? pick_xb<kGemvRmsNorm, FP8>(kh)
                                       : pick_xb<kGemvPlain, FP8>(kh);
   switch (mode) {
-    case kGemvRmsNorm: return pick_kh<kGemvRmsNorm, FP8>(kh, bt, ups);
-    case kGemvSwiGLU: return pick_kh<kGemvSwiGLU, FP8>(kh, bt, ups);
-    case kGemvRmsNormSwiGLU: return pick_kh<kGemvRmsNormSwiGLU, FP8>(kh, bt, ups);
-    default: return pick_kh<kGemvPlain, FP8>(kh, bt, ups);
+    case kGemvRmsNorm: return pick_kh<kGemvRmsNorm, FP8>(kh, bt);
+    case kGemvSwiGLU: return pick_kh<kGemvSwiGLU, FP8>(kh, bt);
+    case kGemvRmsNormSwiGLU: return pick_kh<kGemvRmsNormSwiGLU, FP8>(kh, bt);
+    default: return pick_kh<kGemvPlain, FP8>(kh, bt);
   }
 }
-
 
 // Four groups of 32 batch rows in 4-k-step chunks would spill (256 VGPRs
 // and scratch); that combination takes 2-k-step chunks.
@@ -1159,9 +1142,7 @@ hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
   const bool xb = nwm == 1 && B > kBatchTile && xb_bytes + part32 <= 152 * 1024;
   const int bt = xb || B >= 9 ? 2 : 1;  // batch column tiles held in registers
   const int pass = xb ? 32 : kBatchTile;
-  const int ups = 1;
-  const MfmaFn fn = w.fp8 ? pick_mode<true>(mode, kh, bt, ups, xb)
-                          : pick_mode<false>(mode, kh, bt, ups, xb);
+  const MfmaFn fn = w.fp8 ? pick_mode<true>(mode, kh, bt, xb) : pick_mode<false>(mode, kh, bt, xb);
   // The activation staging of one matrix at two batch tiles without XB (each
   // wave's slice of the pass's rows, 16 bytes per lane per row tile and
   // k-step) shares the partial-sum region.
