@@ -372,6 +372,13 @@ int db_tune(const char* key, int value) {
     if (value != 0 && value != 1 && value != 2 && value != 4)
       return fail(DB_ERR_INVALID, "db_tune: stream_waves must be 0, 1, 2 or 4");
     t.stream_waves = value;
+  } else if (!strcmp(key, "gemv_pass_grid")) {
+    if (value < 0 || value % 8 != 0)
+      return fail(DB_ERR_INVALID, "db_tune: gemv_pass_grid must be 0 (automatic) or a multiple of 8");
+    t.gemv_pass_grid = value;
+  } else if (!strcmp(key, "gemv_xb")) {
+    if (value != 0 && value != 1) return fail(DB_ERR_INVALID, "db_tune: gemv_xb must be 0 or 1");
+    t.gemv_xb = value;
   } else if (!strcmp(key, "f4_min_tiles")) {
     if (value < 1) return fail(DB_ERR_INVALID, "db_tune: f4_min_tiles must be >= 1");
     t.f4_min_tiles = value;

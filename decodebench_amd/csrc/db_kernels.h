@@ -27,6 +27,10 @@ struct Tuning {
   int gemv_long_stage = 0;     // long-row MFMA GEMV x: 0 auto, 1 direct, 2 LDS-staged
   int gemv_pair_min_batch = 0; // gate/up pair rows from which x streams (0: 17)
   int stream_waves = 0;        // db_stream_read waves per workgroup: 0 (4), 1, 2 or 4
+  int gemv_pass_grid = 0;      // one-matrix MFMA GEMV above 16 rows: workgroups per
+                               // 16-row pass (0: CUs / passes; else a multiple of 8)
+  int gemv_xb = 0;             // 1: 32-row passes (rows 16..31 of x in LDS) on the
+                               // full grid instead
 };
 Tuning& tuning();
 

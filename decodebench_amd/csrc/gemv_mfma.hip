@@ -36,9 +36,10 @@
 //    stage rounds, fp16(fp16(x * inv_rms) * gamma) -- x * inv_rms rounded
 //    once rather than through fp32 (see norm_mul) -- gamma read from an LDS
 //    copy.
-// Batches above 16 run as passes (grid.y), each reading the weights: one
-// weight matrix takes 32-row passes when the LDS holds rows 16..31 of x next
-// to the partial sums (XB), otherwise passes are 16 rows.
+// Batches above 16 run as passes of 16 rows (grid.y).  For one weight
+// matrix the passes of a row group run on one XCD at the same time, so the
+// later passes read its weights from L2 (see launch_gemv_mfma); 32-row
+// passes with rows 16..31 of x in LDS (XB) remain as a tuning option.
 // Plain GEMV with longer rows (K a multiple of 2048 above 4096, the down
 // projection) and the gate/up pair above 16 rows, with or without the
 // RMSNorm, take kernels that stream x as well: gemv_mfma_long_kernel and
@@ -170,12 +171,17 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
                                        (int)gridDim.x);
   const unsigned char* wmat[2] = {static_cast<const unsigned char*>(a.w0),
                                   static_cast<const unsigned char*>(a.w1)};
-  // A register set holds one group.  `checked`: skip a group past
-  // my_groups (only outside the steady loop, whose loads are unconditional so
-  // the compiler waits per set).
-  auto load_set = [&](u4 (&dst)[NWM][KW], int j, bool checked) {
-    if (checked && j >= my_groups) return;
-    const int grp = blockIdx.x + gridDim.x * min(j, my_groups - 1);
+  // A register set holds one group; j past the workgroup's last group
+  // re-reads that one.  Every load_set is unconditional: after a load under
+  // a branch the compiler merges the two paths' outstanding loads and waits
+  // for all of them (vmcnt(0)) where one set would do.  With the first
+  // group's load conditional, the normalisation's gamma store and barrier
+  // waited for that group's weights (seen in the ISA); unconditional, they
+  // stay in flight, which made F1 at 16 rows 11.05 -> 9.72 us, F1-QKV at 16
+  // and 32 rows 13.13 -> 11.97 and 16.93 -> 15.92 us, e4m3 F1-QKV at 4-32
+  // rows 4-6% faster (graph back-to-back, interleaved runs).
+  auto load_set = [&](u4 (&dst)[NWM][KW], int j) {
+    const int grp = blockIdx.x + gridDim.x * max(min(j, my_groups - 1), 0);
     const int row = min(grp * kRowsPerGroup + r8, a.N - 1);
 #pragma unroll
     for (int m = 0; m < NWM; ++m)
@@ -283,7 +289,7 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    load_set(wa, 0, true);  // every workgroup owns at least one group
+    load_set(wa, 0);
   } else {
 #pragma unroll
     for (int bt = 0; bt < BT; ++bt) {
@@ -308,7 +314,7 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x and gamma are here
     }
     __builtin_amdgcn_sched_barrier(0);
-    load_set(wa, 0, true);  // every workgroup owns at least one group
+    load_set(wa, 0);
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -420,17 +426,20 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
     u4 wb[NWM][KW];
     int j = 0;
     for (; j + 3 <= my_groups; j += 2) {
-      load_set(wb, j + 1, false);
+      load_set(wb, j + 1);
       consume(wa, j);
-      load_set(wa, j + 2, false);
+      load_set(wa, j + 2);
       consume(wb, j + 1);
     }
-    // Fewer than 3 groups remain; set A holds the first of them.
-    if (j + 1 < my_groups) load_set(wb, j + 1, true);
-    consume(wa, j);
-    if (j + 2 < my_groups) load_set(wa, j + 2, true);
-    if (j + 1 < my_groups) consume(wb, j + 1);
-    if (j + 2 < my_groups) consume(wa, j + 2);
+    // One or two groups remain; set A holds the first.  Each case is
+    // straight-line code (see load_set).
+    if (j + 1 < my_groups) {
+      load_set(wb, j + 1);
+      consume(wa, j);
+      consume(wb, j + 1);
+    } else {
+      consume(wa, j);
+    }
   }
 
   __syncthreads();
@@ -1127,19 +1136,39 @@ hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
   if (long_rows(mode, K)) return launch_gemv_mfma_long(a, w.fp8, cu_count, stream);
   if (pair_rows(mode, B, K, N))
     return launch_gemv_mfma_pair(a, mode == kGemvRmsNormSwiGLU, w.fp8, cu_count, stream);
-  int grid = min(a.groups, cu_count);
-  a.gpw = (a.groups + grid - 1) / grid;
-  if (a.gpw > kMaxGroupsPerWg) a.gpw = kMaxGroupsPerWg;
-  // Spread the groups evenly: every workgroup owns gpw or gpw - 1 groups.
-  grid = (a.groups + a.gpw - 1) / a.gpw;
   const int kh = K / 512;
   const int nwm = gemv_is_swiglu(mode) ? 2 : 1;
-  // Above 16 rows one weight matrix takes 32-row passes when the LDS holds
-  // rows 16..31 of x (16 KB x KH) next to the 32-column partial sums; else
-  // 16-row passes, each reading the weights again.
+  // One weight matrix above 16 rows: P = ceil(B / 16) passes of 16 rows
+  // (grid.y), each on CUs / P workgroups, a multiple of 8.  Workgroup
+  // (x, y) is then linear id x + grid.x * y, so with workgroups dealt to
+  // the 8 XCDs in turn every pass of a row group runs on the same XCD at
+  // the same time, and its weight lines come from HBM once and from that
+  // XCD's L2 for the other passes, while each CU reads 16 rows of x rather
+  // than 32.  Measured on MI355X (graph back-to-back) against 32-row passes
+  // on the full grid (XB below): F1 [4096, 4096] B = 32 16.2 -> 13.2 us,
+  // B = 64 29.8 -> 20.1 us; F1-QKV [6144, 4096] B = 17 17.4 -> 16.7 us,
+  // B = 32 18.0 -> 16.9 us, B = 64 33.5 -> 27.4 us; e4m3 F1-QKV B = 32
+  // 15.5 -> 11.8 us.  A grid that is not a multiple of 8 loses the shared
+  // L2 (B = 48 on 77 workgroups per pass: 28.3 against 27.2 us on 64), and
+  // 8-row passes on twice the workgroups were slower at 16 and 32 rows.
+  const int passes = (B + kBatchTile - 1) / kBatchTile;
+  const bool split_passes = nwm == 1 && passes > 1 && tuning().gemv_xb == 0;
+  int grid = min(a.groups, cu_count);
+  if (split_passes) {
+    const int forced = tuning().gemv_pass_grid;
+    grid = min(a.groups, max(8, (forced > 0 ? forced : cu_count / passes) / 8 * 8));
+  }
+  a.gpw = (a.groups + grid - 1) / grid;
+  if (a.gpw > kMaxGroupsPerWg) a.gpw = kMaxGroupsPerWg;
+  // Spread the groups evenly: every workgroup owns gpw or gpw - 1 groups
+  // (or, on a split-pass grid rounded up to a multiple of 8, at least one).
+  grid = (a.groups + a.gpw - 1) / a.gpw;
+  if (split_passes) grid = min(a.groups, (grid + 7) / 8 * 8);
+  // gemv_xb: 32-row passes when the LDS holds rows 16..31 of x (16 KB x KH)
+  // next to the 32-column partial sums.
   const size_t xb_bytes = (size_t)kWavesM * 2 * kh * kWave * 16;
   const size_t part32 = sizeof(float) * a.gpw * nwm * kWavesM * 32 * kRowsPerGroup;
-  const bool xb = nwm == 1 && B > kBatchTile && xb_bytes + part32 <= 152 * 1024;
+  const bool xb = !split_passes && nwm == 1 && B > kBatchTile && xb_bytes + part32 <= 152 * 1024;
   const int bt = xb || B >= 9 ? 2 : 1;  // batch column tiles held in registers
   const int pass = xb ? 32 : kBatchTile;
   const MfmaFn fn = w.fp8 ? pick_mode<true>(mode, kh, bt, xb) : pick_mode<false>(mode, kh, bt, xb);

@@ -211,8 +211,11 @@ int db_stream_read(const void* src, size_t bytes, int kb_per_wave, unsigned magi
  * or 4; 0 automatic), "gemv_long_stage" (its activations: 1 loaded as B
  * operands, 2 staged through LDS; 0 automatic), "gemv_pair_min_batch"
  * (batch rows from which the gate/up pair streams its activations; 0
- * automatic, 17) and "stream_waves" (db_stream_read's waves per workgroup:
- * 1, 2 or 4; 0 is 4).
+ * automatic, 17), "stream_waves" (db_stream_read's waves per workgroup:
+ * 1, 2 or 4; 0 is 4), "gemv_pass_grid" (one weight matrix above 16 batch
+ * rows on MFMA: workgroups per 16-row pass, a multiple of 8; 0 automatic,
+ * CUs / passes) and "gemv_xb" (1: 32-row passes with rows 16..31 of the
+ * activations in LDS on the full grid instead; 0, the default, off).
  * Process-wide; no counterpart in the reference. */
 int db_tune(const char* key, int value);
 

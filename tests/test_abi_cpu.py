@@ -181,6 +181,11 @@ def test_tune_keys(lib):
     assert lib.db_tune(b"gemv_pair_min_batch", 0) == 0
     assert lib.db_tune(b"gemv_long_gpw", 7) == -1
     assert lib.db_tune(b"gemv_pair_tiles", 0) == -1
+    assert lib.db_tune(b"gemv_pass_grid", 12) == -1
+    assert lib.db_tune(b"gemv_pass_grid", -8) == -1
+    assert lib.db_tune(b"gemv_pass_grid", 0) == 0
+    assert lib.db_tune(b"gemv_xb", 2) == -1
+    assert lib.db_tune(b"gemv_xb", 0) == 0
     assert lib.db_tune(b"f4_merge", 0) == 0
     assert lib.db_tune(b"f4_blocks_per_cu", 2) == 0
     assert lib.db_tune(b"f4_blocks_per_cu", 1) == 0   # back to the default

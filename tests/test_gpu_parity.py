@@ -141,8 +141,9 @@ MFMA_CASES = [
     ("f2", 4, 4096, 14336), ("f2", 32, 4096, 1792), ("f2", 9, 2048, 777),
     ("plain", 16, 4096, 4100), ("plain", 3, 2048, 8), ("f2", 3, 4096, 1000),
     ("f2", 3, 2048, 515),
-    # 32-row passes of one matrix (rows 16..31 of x in LDS): the QKV shape at
-    # B=32, ragged batches, two passes (B=40), K=2048 with more groups
+    # one matrix above 16 rows (16-row passes sharing the weights through an
+    # XCD's L2): the QKV shape at B=32, ragged batches, three passes (B=40),
+    # K=2048 with more groups
     ("f1", 32, 4096, 6144), ("plain", 24, 4096, 4096), ("f1", 21, 2048, 1000),
     ("plain", 40, 2048, 3000), ("plain", 32, 4096, 2040),
 ]
@@ -193,6 +194,40 @@ def test_mfma_and_valu_gemv_paths_agree():
         lib.db_tune(b"gemv_mfma_min_batch", 0)
     for a, b in zip(*outs):
         assert rel_l2(a.float().cpu().numpy(), b.float().cpu().numpy()) < 1e-3
+
+
+def test_one_matrix_pass_shapes_agree():
+    """One weight matrix above 16 rows: 16-row passes on the default split
+    grid, on 8 to 256 workgroups per pass, and 32-row passes with rows 16..31
+    of x in LDS (gemv_xb) agree to fp32 summation order, fp16 and e4m3, with
+    and without the RMSNorm."""
+    from decodebench_amd.quant import quantize_e4m3_rows
+
+    gen = torch.Generator().manual_seed(81)
+    lib = ops.load_library()
+    try:
+        for B, K, N in ((17, 4096, 6144), (32, 4096, 4096), (40, 2048, 1000), (64, 4096, 520)):
+            print(f"[passes] B={B} K={K} N={N}", flush=True)
+            x = randn(gen, (B, K)).cuda()
+            g = randn(gen, (K,), std=0.1, mean=1.0).cuda()
+            W = randn(gen, (N, K), std=0.02)
+            Wq, s = (t.cuda() for t in quantize_e4m3_rows(W))
+            W = W.cuda()
+
+            def run():
+                return (ops.f1_rmsnorm_gemv(x, g, W), ops.gemv(x, W),
+                        ops.f1_rmsnorm_gemv(x, g, Wq, w_scale=s), ops.gemv(x, Wq, w_scale=s))
+
+            base = run()
+            for xb, grid in ((1, 0), (0, 8), (0, 64), (0, 256)):
+                assert lib.db_tune(b"gemv_xb", xb) == 0
+                assert lib.db_tune(b"gemv_pass_grid", grid) == 0
+                for a, b in zip(run(), base):
+                    err = rel_l2(a.float().cpu().numpy(), b.float().cpu().numpy())
+                    assert err < 1e-3, f"B={B} K={K} N={N} xb={xb} grid={grid}: rel-L2 {err:.2e}"
+    finally:
+        lib.db_tune(b"gemv_xb", 0)
+        lib.db_tune(b"gemv_pass_grid", 0)
 
 
 # --------------------------------------------------- long rows (MFMA, streamed x)
