@@ -1058,17 +1058,27 @@ static hipError_t launch_gemv_mfma_long(const MfmaArgs& a0, bool fp8, int cu_cou
   // at 32 rows the 4-k-step sets spill.
   int kc = tuning().gemv_long_kc;
   if (kc == 0) kc = fp8 && bt == 1 ? 4 : 2;
+  // Row groups per workgroup: the fewest (1, 2 or 4) that put every pass's
+  // workgroups on the CUs at once.  Above 32 rows the passes of a row group
+  // then run side by side on one XCD (grid.x a multiple of 8, as in
+  // launch_gemv_mfma) and share its L2 copy of the weights: [4096, 14336]
+  // on 128 workgroups of 4 groups per pass against 256 of 2: fp16 B = 64
+  // 64.1 -> 48.6 us, B = 96 97.5 -> 91.9 us, e4m3 B = 33-64 42-47 -> 33 us.
+  // At one pass, 4 groups per workgroup on half the CUs measured slower
+  // (fp16 B = 32 32.3 -> 45.7 us).
+  const int passes = (a.B + 8 * bt - 1) / (8 * bt);
   int gpw = tuning().gemv_long_gpw;
   if (gpw == 0) {
     gpw = 4;
     for (int g = 1; g < 4; g *= 2)
-      if ((a.groups + g - 1) / g <= cu_count) {
+      if ((a.groups + g - 1) / g * passes <= cu_count) {
         gpw = g;
         break;
       }
   }
   a.gpw = gpw;
-  const int grid = (a.groups + gpw - 1) / gpw;
+  int grid = (a.groups + gpw - 1) / gpw;
+  if (passes > 1) grid = min(a.groups, (grid + 7) / 8 * 8);
   if (bt == 4 && gpw == 4) kc = 2;
   const bool xs = tuning().gemv_long_stage != 1;
   const MfmaFn fn = fp8 ? pick_long<true>(kc, bt, gpw, xs) : pick_long<false>(kc, bt, gpw, xs);
