@@ -11,7 +11,8 @@
 // multiply-adds.
 //
 // Decomposition
-//  * One persistent workgroup per CU, 8 waves.  Each wave owns one K-slice
+//  * One persistent workgroup per CU and pass, 8 waves (above 16 rows the
+//    passes split the CUs, see launch_gemv_mfma).  Each wave owns one K-slice
 //    (K / 8 columns) of every weight row, split into halves h = 0, 1.
 //  * Weight rows are taken in groups of 8, which spreads N / 8 groups evenly
 //    over the CUs at N = 4096, 6144 and 14336.  One v_mfma_f32_16x16x32_f16
@@ -110,11 +111,12 @@ struct MfmaArgs {
 // of two k-steps after v_cvt_scalef32_pk_f16_fp8 widening.  The activations
 // are loaded in the same column order, so the dot products are unchanged;
 // the row scales multiply the reduced sums in the epilogue.
-// XB (one weight matrix, BT = 2): a pass is 32 batch rows.  Rows 16..31 get
-// two more column tiles whose activation slices are written once to LDS
-// (each wave its own, 16 KB x KH / 8 per wave) and read back per group, so
-// every weight tile feeds 32 rows instead of being re-read by a second
-// 16-row pass.
+// XB (one weight matrix, BT = 2; a tuning option, db_tune("gemv_xb", 1)): a
+// pass is 32 batch rows.  Rows 16..31 get two more column tiles whose
+// activation slices are written once to LDS (each wave its own, 16 KB x KH /
+// 8 per wave) and read back per group, so every weight tile feeds 32 rows in
+// one workgroup; the default instead runs two 16-row passes that share the
+// weights through an XCD's L2.
 template <int MODE, int KH, int BT, bool FP8, bool XB>
 __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   constexpr int NWM = gemv_is_swiglu(MODE) ? 2 : 1;
