@@ -1161,8 +1161,9 @@ hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
   // B = 64 29.8 -> 20.1 us; F1-QKV [6144, 4096] B = 17 17.4 -> 16.7 us,
   // B = 32 18.0 -> 16.9 us, B = 64 33.5 -> 27.4 us; e4m3 F1-QKV B = 32
   // 15.5 -> 11.8 us.  A grid that is not a multiple of 8 loses the shared
-  // L2 (B = 48 on 77 workgroups per pass: 28.3 against 27.2 us on 64), and
-  // 8-row passes on twice the workgroups were slower at 16 and 32 rows.
+  // L2 (F1-QKV B = 48 on 77 workgroups per pass: 28.3 against 23.8 us on
+  // 80), and 8-row passes on twice the workgroups were slower at 16 and 32
+  // rows.
   const int passes = (B + kBatchTile - 1) / kBatchTile;
   const bool split_passes = nwm == 1 && passes > 1 && tuning().gemv_xb == 0;
   int grid = min(a.groups, cu_count);
