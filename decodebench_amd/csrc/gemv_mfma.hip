@@ -423,8 +423,8 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
 
   {
     // Two register sets; the steady loop loads and consumes set B inside
-    // one iteration (see flashdecode.hip for why that matters to the
-    // compiler).
+    // one iteration, which keeps the compiler from draining all loads at
+    // the loop header.
     u4 wb[NWM][KW];
     int j = 0;
     for (; j + 3 <= my_groups; j += 2) {
