@@ -146,6 +146,9 @@ MFMA_CASES = [
     # K=2048 with more groups
     ("f1", 32, 4096, 6144), ("plain", 24, 4096, 4096), ("f1", 21, 2048, 1000),
     ("plain", 40, 2048, 3000), ("plain", 32, 4096, 2040),
+    # the norm at one batch tile with x staged through LDS: K=2048 (two rows
+    # per load), a partial tile
+    ("f1", 5, 2048, 520), ("f1", 8, 4096, 6144),
 ]
 
 
@@ -477,6 +480,7 @@ FP8_CASES = [
     ("f2n", 9, 2048, 100), ("plain", 3, 2048, 8), ("plain", 16, 4096, 4100),
     ("f2", 2, 4096, 520), ("f2n", 2, 4096, 1000),
     ("f1", 32, 4096, 6144), ("plain", 20, 4096, 777), ("f1", 40, 2048, 520),
+    ("f1", 6, 2048, 333), ("f1", 8, 4096, 4096),
 ]
 
 
