@@ -13,8 +13,8 @@ namespace dbk {
 struct Tuning {
   int gemv_waves_per_cu = 0;   // 0: the default, 32 waves per CU
   int gemv_mfma_min_batch = 0; // smallest batch that takes the MFMA GEMV
-                               // (0: 3 for one weight matrix, 4 for the
-                               // gate/up pair -- the measured crossovers)
+                               // (0: the measured crossovers, 2 or 3 rows
+                               // by mode and weight type, see launch_gemv)
   int f4_blocks_per_cu = 1;    // target F4 workgroups per CU
   int f4_min_tiles = 8;        // minimum 16-row tiles per F4 split
   int f4_waves = 0;            // waves per F4 workgroup (4 or 8; 0: auto)

@@ -4,8 +4,9 @@
 // + SwiGLU pair of the decode-layer chain and the plain projection share one
 // kernel template (gemv_valu.h).  This file instantiates its fp16-weight half
 // and chooses the launch shape; gemv_fp8.hip instantiates the e4m3 half, and
-// batches from 3 rows (2 for the e4m3 gate/up pair) go to the MFMA kernel
-// (gemv_mfma.hip): the crossovers measured on MI355X at K = 4096.
+// batches from 3 rows (2 for the e4m3 norm and gate/up modes and for plain
+// rows longer than 4096) go to the MFMA kernels (gemv_mfma.hip): the
+// crossovers measured on MI355X.
 #include <mutex>
 #include <unordered_map>
 
@@ -83,10 +84,17 @@ hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
                        const GemvWeights& w, void* y, int B, int K, int N, float eps,
                        int cu_count, hipStream_t stream) {
   const int forced_min = tuning().gemv_mfma_min_batch;
-  // Measured at K = 4096 (graph back-to-back): the VALU kernel wins at 2
-  // rows except for the e4m3 gate/up pair (22.4 vs 19.2 us); at 3 rows it
-  // would run two 2-row passes, 1.5-1.8x the MFMA time.
-  const int auto_min = gemv_is_swiglu(mode) && w.fp8 ? 2 : 3;
+  // At 3 rows the VALU kernel would run two 2-row passes, 1.5-1.8x the MFMA
+  // time.  At 2 rows (graph back-to-back, us, VALU / MFMA) MFMA takes the
+  // e4m3 modes with a norm or two matrices (F1 [4096, 4096] 5.87 / 5.46,
+  // F1-QKV 7.17 / 6.81, gate/up pair 22.4 / 19.2, RMSNorm -> gate/up 23.2 /
+  // 19.8) and rows longer than 4096 (down projection [4096, 14336] fp16
+  // 20.9 / 20.1, e4m3 14.0 / 11.7); the VALU kernel keeps fp16 F1 (7.72 /
+  // 7.88; F1-QKV 10.36 / 10.16-10.46), the fp16 pair (35.4 / 36.9,
+  // RMSNorm -> gate/up 36.5 / 36.8) and the plain projection at K = 4096
+  // (fp16 6.95 / 7.24, e4m3 4.54 / 5.11).
+  const bool mfma_at_two = (w.fp8 && mode != kGemvPlain) || (mode == kGemvPlain && K > 4096);
+  const int auto_min = mfma_at_two ? 2 : 3;
   const int mfma_min = forced_min > 0 ? forced_min : auto_min;
   if (B >= mfma_min && gemv_mfma_supported(mode, B, K, N))
     return launch_gemv_mfma(mode, x, gamma, w, y, B, K, N, eps, cu_count, stream);

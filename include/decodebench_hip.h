@@ -196,8 +196,9 @@ int db_stream_read(const void* src, size_t bytes, int kb_per_wave, unsigned magi
                    unsigned* sink, void* stream);
 
 /* Launch-geometry knobs for tuning sweeps: "gemv_waves_per_cu" (<= 0: the
- * default, 32), "gemv_mfma_min_batch" (0: automatic, 3 rows, 2 for the
- * e4m3 gate/up pair), "f4_blocks_per_cu", "f4_min_tiles",
+ * default, 32), "gemv_mfma_min_batch" (0: automatic, 3 rows; 2 for the
+ * e4m3 norm and gate/up modes and for plain rows longer than 4096),
+ * "f4_blocks_per_cu", "f4_min_tiles",
  * "f4_waves" (4 or 8 waves per workgroup, 0: automatic), "f4_merge" (0: the
  * split merge runs in a second launch, the default; 1: in the same launch)
  * "f4_line" (F4 score-operand layout: 0 automatic, 1 whole-line K loads,

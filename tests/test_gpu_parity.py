@@ -243,6 +243,8 @@ LONG_CASES = [
     ("f16", 9, 8192, 4100), ("f16", 40, 6144, 520), ("f16", 12, 14336, 7),
     ("fp8", 8, 14336, 4096), ("fp8", 32, 14336, 2048), ("fp8", 17, 28672, 300),
     ("fp8", 5, 6144, 9), ("fp8", 33, 10240, 264),
+    # two rows, which take this kernel too
+    ("f16", 2, 14336, 4096), ("fp8", 2, 14336, 1000),
 ]
 
 
@@ -481,6 +483,8 @@ FP8_CASES = [
     ("f2", 2, 4096, 520), ("f2n", 2, 4096, 1000),
     ("f1", 32, 4096, 6144), ("plain", 20, 4096, 777), ("f1", 40, 2048, 520),
     ("f1", 6, 2048, 333), ("f1", 8, 4096, 4096),
+    # two rows on the MFMA kernel: e4m3 F1 (the QKV shape and a ragged one)
+    ("f1", 2, 4096, 6144), ("f1", 2, 2048, 1001),
 ]
 
 
