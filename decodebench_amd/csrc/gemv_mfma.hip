@@ -207,15 +207,17 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   // faster (F1-QKV B = 16 14.5 -> 13.0 us, B = 32 21.7 -> 19.0 us, F1
   // B = 16 12.6 -> 10.9 us, e4m3 F1-QKV B = 16 10.8 -> 9.7 us), while the
   // gate/up pair at B = 16 (1.1 us) loses: there the weights, not x, set the
-  // pace, and the staging delays their first requests.  At 3-8 rows (one
-  // batch tile) the norm modes stage too, since their weights stay in
-  // flight through the normalisation (F1-QKV B = 3 10.70 -> 10.28 us, B = 8
+  // pace, and the staging delays their first requests.  The norm modes
+  // stage at every batch, since their weights stay in flight through the
+  // normalisation: F1 at 3-8 rows (F1-QKV B = 3 10.70 -> 10.28 us, B = 8
   // 10.86 -> 10.32 us, F1 B = 8 8.55 -> 7.96 us, e4m3 F1-QKV B = 8 7.79 ->
-  // 6.97 us, e4m3 F1 B = 8 6.40 -> 5.54 us); the plain projection there
-  // would wait for the staging barrier and does not (+0.4-0.6 us at 3-4
-  // rows, even at 8).  The staging area is the wave's XB tiles, or the
-  // partial-sum region, which nothing writes before the prologue's barrier.
-  constexpr bool kStage = NWM == 1 && (BT == 2 || gemv_has_norm(MODE));
+  // 6.97 us, e4m3 F1 B = 8 6.40 -> 5.54 us) and RMSNorm -> gate/up at 3-16
+  // rows (fp16 B = 8 37.7 -> 36.8 us, B = 16 39.8 -> 38.5 us, e4m3 B = 16
+  // 23.2 -> 21.8 us).  The plain projection at one batch tile would wait for
+  // the staging barrier and does not (+0.4-0.6 us at 3-4 rows, even at 8).
+  // The staging area is the wave's XB tiles, or the partial-sum region,
+  // which nothing writes before the prologue's barrier.
+  constexpr bool kStage = gemv_has_norm(MODE) || (NWM == 1 && BT == 2);
   const u4 zero4 = {0, 0, 0, 0};
   u4 xr[BT][KH];
   u4 xb[XB ? 2 : 1][KH];  // XB: rows 16..31 (norm modes: for their x^2 sums)
@@ -1190,10 +1192,10 @@ hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
   const int bt = xb || B >= 9 ? 2 : 1;  // batch column tiles held in registers
   const int pass = xb ? 32 : kBatchTile;
   const MfmaFn fn = w.fp8 ? pick_mode<true>(mode, kh, bt, xb) : pick_mode<false>(mode, kh, bt, xb);
-  // The activation staging of one matrix (at one batch tile only with the
-  // norm) without XB -- each wave's slice of the pass's rows, 16 bytes per
+  // The activation staging (the norm modes, and one matrix at two batch
+  // tiles) without XB -- each wave's slice of the pass's rows, 16 bytes per
   // lane per row tile and k-step -- shares the partial-sum region.
-  const bool staged = nwm == 1 && (bt == 2 || gemv_has_norm(mode));
+  const bool staged = gemv_has_norm(mode) || (nwm == 1 && bt == 2);
   const size_t stage_bytes = staged ? (size_t)kWavesM * bt * kh * kWave * 16 : 0;
   const size_t part16 = sizeof(float) * a.gpw * nwm * kWavesM * 8 * bt * kRowsPerGroup;
   const size_t lds = xb ? xb_bytes + part32 : (part16 > stage_bytes ? part16 : stage_bytes);

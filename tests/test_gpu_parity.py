@@ -444,7 +444,10 @@ def test_gemv_edge_shapes(mode, B, K, N, dtype):
 # One kernel for the decode chain's post-attention half; batch 1 takes the
 # VALU kernel, batches of 2..16 (and passes of 16) the MFMA kernel.
 F2N_CASES = [(1, 4096, 14336), (1, 1024, 300), (1, 4104, 64), (4, 4096, 1000),
-             (17, 4096, 600), (2, 2048, 777), (9, 512, 40)]
+             (17, 4096, 600), (2, 2048, 777), (9, 512, 40),
+             # x staged through LDS on the batched kernel: one and two batch
+             # tiles at K = 2048 and 4096, up to 7 row groups per workgroup
+             (3, 2048, 333), (12, 2048, 520), (16, 4096, 14336)]
 
 
 @pytest.mark.parametrize("B,K,N", F2N_CASES)
