@@ -641,18 +641,41 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_long_kernel(MfmaArgs a) {
   };
 
   u4 xa[kXL], wa[GPW][KWC], xb[kXL], wb[GPW][KWC];
+  // Left to itself the compiler issued set B's loads only after consume(A)
+  // had waited for all of set A (vmcnt(0) at the loop header, read in the
+  // ISA), so one chunk was in flight at a time.  A scheduling barrier after
+  // each load keeps the next chunk in flight, and the tail is straight-line
+  // code per case (a load under a branch merges two paths into a vmcnt(0)).
+  // Measured with fp16 weights ([4096, 14336], µs): B = 3 19.6 -> 19.2,
+  // B = 32 32.0 -> 30.9, B = 48 53.5 -> 46.8 (its register spill shrank
+  // from 44 to 12 bytes), B = 64 48.3 -> 45.6.  The e4m3 kernels keep the
+  // compiler's order: the barrier cost 0.4 us at B = 16, and the split tail
+  // added a spill to 32 rows x 4 groups (B = 48-64 +2 us).  32 rows x 4
+  // groups take no barrier (it raised the spill).
+  constexpr bool kPrefetchFirst = !FP8 && BT * GPW < 16;
   load(xa, wa, 0);
   int c = 0;
   for (; c + 3 <= nch; c += 2) {
     load(xb, wb, c + 1);
+    if constexpr (kPrefetchFirst) __builtin_amdgcn_sched_barrier(0);
     consume(xa, wa);
     load(xa, wa, c + 2);
+    if constexpr (kPrefetchFirst) __builtin_amdgcn_sched_barrier(0);
     consume(xb, wb);
   }
   // One or two chunks remain; set A holds the first.
-  if (c + 1 < nch) load(xb, wb, c + 1);
-  consume(xa, wa);
-  if (c + 1 < nch) consume(xb, wb);
+  if constexpr (FP8) {
+    if (c + 1 < nch) load(xb, wb, c + 1);
+    consume(xa, wa);
+    if (c + 1 < nch) consume(xb, wb);
+  } else if (c + 1 < nch) {
+    load(xb, wb, c + 1);
+    if constexpr (kPrefetchFirst) __builtin_amdgcn_sched_barrier(0);
+    consume(xa, wa);
+    consume(xb, wb);
+  } else {
+    consume(xa, wa);
+  }
 
   // D[4 g4 + i][c16]: rows 0..7 x batch 0..7 (half 0) in lanes (g4 < 2,
   // c16 < 8), their half-1 partners 40 lanes higher.
@@ -874,15 +897,29 @@ __global__ __launch_bounds__(WV * kWave) void gemv_mfma_tile16_kernel(MfmaArgs a
     }
   }
   int c = 0;
+  // A scheduling barrier after each load keeps the next chunk in flight
+  // while the current one is consumed (otherwise the compiler sinks the
+  // loads below the current chunk's waits), and the tail is straight-line
+  // code per case.  Measured at [14336, 4096], 17-32 rows (µs): fp16 pair
+  // 39.7 -> 39.2 (B = 17), 42.1 -> 41.8 (B = 32); RMSNorm -> gate/up 46.4
+  // -> 44.8, 50.3 -> 48.9; e4m3 pair 27.9 -> 27.4 (B = 32), RMSNorm ->
+  // gate/up 32.6 -> 31.3, 36.3 -> 34.8.
   for (; c + 3 <= nch; c += 2) {
     load(xb, gb, wb, c + 1);
+    __builtin_amdgcn_sched_barrier(0);
     consume(xa, ga, wa);
     load(xa, ga, wa, c + 2);
+    __builtin_amdgcn_sched_barrier(0);
     consume(xb, gb, wb);
   }
-  if (c + 1 < nch) load(xb, gb, wb, c + 1);
-  consume(xa, ga, wa);
-  if (c + 1 < nch) consume(xb, gb, wb);
+  if (c + 1 < nch) {
+    load(xb, gb, wb, c + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    consume(xa, ga, wa);
+    consume(xb, gb, wb);
+  } else {
+    consume(xa, ga, wa);
+  }
 
   // D[4 g4 + i][c16] = tile row 4 g4 + i (group 2j + (g4 >> 1), row
   // 4 (g4 & 1) + i) against batch row 16 bt + c16.
