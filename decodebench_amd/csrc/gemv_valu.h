@@ -139,7 +139,6 @@ __global__ __launch_bounds__(WV * kWave) void gemv_kernel(GemvArgs a) {
 
   const unsigned char* wmat[2] = {static_cast<const unsigned char*>(a.w0),
                                   static_cast<const unsigned char*>(a.w1)};
-  const float* smat[2] = {a.s0, a.s1};
 
   // ---- tile loader: R rows x U chunks per lane (x2 for SwiGLU), issued in
   // the order consume() uses them (chunk-major), so each wait is for the
@@ -167,7 +166,13 @@ __global__ __launch_bounds__(WV * kWave) void gemv_kernel(GemvArgs a) {
     }
     if constexpr (FP8) {
       const int sl = lane % (NW * R);
-      sc = smat[sl / R][min(g * R + sl % R, a.N - 1)];
+      // A select of the two kernel-argument pointers, not an index into a
+      // local pointer array: the compiler then knows the scales are global
+      // memory.  Through the array it issued a flat load, after which every
+      // wait became vmcnt(0), and the activation staging waited for the
+      // whole first weight tile (read in the ISA).
+      const float* sp = sl < R ? a.s0 : a.s1;
+      sc = sp[min(g * R + sl % R, a.N - 1)];
     }
   };
 
