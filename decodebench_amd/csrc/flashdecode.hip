@@ -318,10 +318,10 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
   // header.)  Measured on MI355X against sets of two tiles (two to four in
   // flight): 24.5 vs 25.0 us at batch 1, L = 32768, and 1-1.5% faster at
   // batch 4 and 8; deeper queues per wave only spread the tiles' arrival
-  // times and lengthen the tail of the slowest wave.  DEPTH 1 (the batch-1
-  // whole-line kernel over long splits) waits for the oldest tile before
-  // requesting the next, so each wave keeps one tile in flight while it
-  // computes: at batch 1, L = 32768 (8 tiles per wave) 24.2 -> 24.0 us.
+  // times and lengthen the tail of the slowest wave.  DEPTH 1 (a tuning
+  // option for the 8-wave whole-line kernel) waits for the oldest tile
+  // before requesting the next, so each wave keeps one tile in flight while
+  // it computes.
   // Timestamps of an instrumented copy there show the waves of one
   // workgroup finishing up to 4-6 us apart; handing tiles out from an LDS
   // counter instead of the fixed w, w + NW, ... walk (so that faster waves
@@ -680,13 +680,12 @@ hipError_t launch_f4(const void* q, const void* k, const void* v, void* o,
   const int tiles_per_wave = (a.tps + waves - 1) / waves;
   const bool line = tuning().f4_line == 1 ||
                     (tuning().f4_line == 0 && (tiles_per_wave <= 2 || pairs <= 8));
-  // One tile in flight per wave for the whole-line kernel once its waves
-  // walk 4 or more tiles (measured on MI355X at batch 1, L = 32768: 24.2 ->
-  // 24.0 us); with 1-2 tiles per wave, and at L = 8192, both tiles are
-  // requested at once (one in flight was 0.3 us slower at L = 1024).
-  const int depth = tuning().f4_depth > 0
-                        ? tuning().f4_depth
-                        : (line && waves == 8 && tiles_per_wave >= 4 ? 1 : 2);
+  // Two tiles in flight per wave.  One (DEPTH 1, db_tune("f4_depth", 1))
+  // was 0.2 us faster at batch 1, L = 32768 until the two-tile tail became
+  // straight-line code; since then it is slower there (24.00 against 23.76
+  // us) and at L = 16384 (14.85 against 14.48 us), and 0.3 us slower at
+  // L = 1024.
+  const int depth = tuning().f4_depth > 0 ? tuning().f4_depth : 2;
   hipLaunchKernelGGL(pick_kernel(G, waves, line, depth), dim3(pairs * a.S),
                      dim3(waves * kWave), 0, stream, a);
   if (a.S > 1 && !a.fused_merge) {
