@@ -14,17 +14,21 @@
 #include <atomic>
 
 #include "../../include/decodebench_hip.h"
+#include "../../include/decodebench_hip_tuning.h"
 #include "db_kernels.h"
 
 namespace dbk {
 
+// The knobs are per host thread: a value one thread sets through db_tune
+// changes only the launches that thread makes.
 Tuning& tuning() {
-  static Tuning t;
+  static thread_local Tuning t;
   return t;
 }
 
-int device_cu_count(int* err) {
-  static std::atomic<int> cache[64];
+namespace {
+// A positive device attribute of the current device, cached per device.
+int device_attribute(hipDeviceAttribute_t attr, std::atomic<int> (&cache)[64], int* err) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) {
@@ -33,17 +37,31 @@ int device_cu_count(int* err) {
   }
   if (dev >= 0 && dev < 64) {
     const int c = cache[dev].load(std::memory_order_relaxed);
-    if (c > 0) return c;
+    if (c > 0) {
+      *err = 0;
+      return c;
+    }
   }
-  int cus = 0;
-  e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  if (e != hipSuccess || cus <= 0) {
+  int value = 0;
+  e = hipDeviceGetAttribute(&value, attr, dev);
+  if (e != hipSuccess || value <= 0) {
     *err = e != hipSuccess ? (int)e : (int)hipErrorInvalidValue;
     return 0;
   }
-  if (dev >= 0 && dev < 64) cache[dev].store(cus, std::memory_order_relaxed);
+  if (dev >= 0 && dev < 64) cache[dev].store(value, std::memory_order_relaxed);
   *err = 0;
-  return cus;
+  return value;
+}
+}  // namespace
+
+int device_cu_count(int* err) {
+  static std::atomic<int> cache[64];
+  return device_attribute(hipDeviceAttributeMultiprocessorCount, cache, err);
+}
+
+int device_xcc_count(int* err) {
+  static std::atomic<int> cache[64];
+  return device_attribute(hipDeviceAttributeNumberOfXccs, cache, err);
 }
 
 int f4_max_splits(int G);
@@ -239,6 +257,60 @@ int f4_effective_splits(int L, int S) {
   return S < ntiles ? S : ntiles;
 }
 
+// The launch-geometry knobs of db_tune / db_tune_get: name, field, the
+// values accepted (checked before anything changes) and, for one knob, how
+// a value is stored.
+struct Knob {
+  const char* name;
+  int dbk::Tuning::*field;
+  bool (*valid)(int);
+  const char* rule;
+  int (*normalise)(int);
+};
+
+const Knob kKnobs[] = {
+    {"gemv_waves_per_cu", &dbk::Tuning::gemv_waves_per_cu, [](int) { return true; },
+     "any value (<= 0: the default)", [](int v) { return v > 0 ? v : 0; }},
+    {"gemv_mfma_min_batch", &dbk::Tuning::gemv_mfma_min_batch,
+     [](int v) { return v == 0 || v >= 2; }, "0 (automatic) or >= 2", nullptr},
+    {"f4_blocks_per_cu", &dbk::Tuning::f4_blocks_per_cu, [](int v) { return v >= 1; }, ">= 1",
+     nullptr},
+    {"f4_min_tiles", &dbk::Tuning::f4_min_tiles, [](int v) { return v >= 1; }, ">= 1", nullptr},
+    {"f4_waves", &dbk::Tuning::f4_waves, [](int v) { return v == 0 || v == 4 || v == 8; },
+     "0, 4 or 8", nullptr},
+    {"f4_merge", &dbk::Tuning::f4_merge, [](int v) { return v >= 0 && v <= 2; },
+     "0 (automatic), 1 (in the same launch where possible) or 2 (second launch)", nullptr},
+    {"f4_misplace", &dbk::Tuning::f4_misplace, [](int v) { return v >= 0; },
+     ">= 0 (0: off)", nullptr},
+    {"f4_line", &dbk::Tuning::f4_line, [](int v) { return v >= 0 && v <= 2; },
+     "0 (auto), 1 (whole lines) or 2", nullptr},
+    {"f4_combine_groups", &dbk::Tuning::f4_combine_groups,
+     [](int v) { return v == 0 || v == 1 || v == 2 || v == 4 || v == 8; }, "0, 1, 2, 4 or 8",
+     nullptr},
+    {"f4_depth", &dbk::Tuning::f4_depth, [](int v) { return v >= 0 && v <= 2; }, "0, 1 or 2",
+     nullptr},
+    {"gemv_long_kc", &dbk::Tuning::gemv_long_kc, [](int v) { return v == 0 || v == 2 || v == 4; },
+     "0, 2 or 4", nullptr},
+    {"gemv_long_gpw", &dbk::Tuning::gemv_long_gpw,
+     [](int v) { return v == 0 || v == 1 || v == 2 || v == 4; }, "0, 1, 2 or 4", nullptr},
+    {"gemv_long_stage", &dbk::Tuning::gemv_long_stage, [](int v) { return v >= 0 && v <= 2; },
+     "0, 1 or 2", nullptr},
+    {"gemv_pair_min_batch", &dbk::Tuning::gemv_pair_min_batch,
+     [](int v) { return v == 0 || v >= 2; }, "0 (automatic) or >= 2", nullptr},
+    {"stream_waves", &dbk::Tuning::stream_waves,
+     [](int v) { return v == 0 || v == 1 || v == 2 || v == 4; }, "0, 1, 2 or 4", nullptr},
+    {"gemv_pass_grid", &dbk::Tuning::gemv_pass_grid, [](int v) { return v >= 0 && v % 8 == 0; },
+     "0 (automatic) or a multiple of 8", nullptr},
+    {"gemv_xb", &dbk::Tuning::gemv_xb, [](int v) { return v == 0 || v == 1; }, "0 or 1",
+     nullptr},
+};
+
+const Knob* find_knob(const char* key) {
+  for (const Knob& k : kKnobs)
+    if (!strcmp(k.name, key)) return &k;
+  return nullptr;
+}
+
 }  // namespace
 
 extern "C" {
@@ -258,7 +330,10 @@ int db_f4_splitkv(const void* q, const void* k, const void* v, void* o,
       return fail(DB_ERR_INVALID, "%s: workspace %zu bytes < %zu required", fn, ws_bytes,
                   need);
   }
-  return hip_status(dbk::launch_f4(q, k, v, o, ws, B, Hq, Hkv, L, D, S, scale,
+  int err = 0;
+  const int nxcc = dbk::device_xcc_count(&err);
+  if (err) return hip_status((hipError_t)err, fn);
+  return hip_status(dbk::launch_f4(q, k, v, o, ws, B, Hq, Hkv, L, D, S, scale, nxcc,
                                    (hipStream_t)stream),
                     fn);
 }
@@ -281,7 +356,7 @@ int db_f4_splitkv_noalloc(const void* q, const void* k, const void* v, void* o,
     const hipError_t e = dbk::f4_scratch_address(&ws);
     if (e != hipSuccess) return hip_status(e, fn);
   }
-  return hip_status(dbk::launch_f4(q, k, v, o, ws, B, Hq, Hkv, L, D, s_eff, scale,
+  return hip_status(dbk::launch_f4(q, k, v, o, ws, B, Hq, Hkv, L, D, s_eff, scale, /*nxcc=*/1,
                                    (hipStream_t)stream, /*allow_fused_merge=*/false),
                     fn);
 }
@@ -322,69 +397,32 @@ int db_null_kernel(void* stream) {
 
 int db_tune(const char* key, int value) {
   if (!key) return fail(DB_ERR_INVALID, "db_tune: null key");
-  dbk::Tuning& t = dbk::tuning();
-  if (!strcmp(key, "gemv_waves_per_cu")) {
-    t.gemv_waves_per_cu = value > 0 ? value : 0;
-  } else if (!strcmp(key, "gemv_mfma_min_batch")) {
-    if (value < 0 || value == 1)
-      return fail(DB_ERR_INVALID, "db_tune: gemv_mfma_min_batch must be 0 (automatic) or >= 2");
-    t.gemv_mfma_min_batch = value;
-  } else if (!strcmp(key, "f4_blocks_per_cu")) {
-    if (value < 1) return fail(DB_ERR_INVALID, "db_tune: f4_blocks_per_cu must be >= 1");
-    t.f4_blocks_per_cu = value;
-  } else if (!strcmp(key, "f4_waves")) {
-    if (value != 0 && value != 4 && value != 8)
-      return fail(DB_ERR_INVALID, "db_tune: f4_waves must be 0, 4 or 8");
-    t.f4_waves = value;
-  } else if (!strcmp(key, "f4_merge")) {
-    if (value != 0 && value != 1)
-      return fail(DB_ERR_INVALID, "db_tune: f4_merge must be 0 or 1");
-    t.f4_merge = value;
-  } else if (!strcmp(key, "f4_line")) {
-    if (value < 0 || value > 2)
-      return fail(DB_ERR_INVALID, "db_tune: f4_line must be 0 (auto), 1 (whole lines) or 2");
-    t.f4_line = value;
-  } else if (!strcmp(key, "f4_combine_groups")) {
-    if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8)
-      return fail(DB_ERR_INVALID, "db_tune: f4_combine_groups must be 0, 1, 2, 4 or 8");
-    t.f4_combine_groups = value;
-  } else if (!strcmp(key, "f4_depth")) {
-    if (value < 0 || value > 2)
-      return fail(DB_ERR_INVALID, "db_tune: f4_depth must be 0, 1 or 2");
-    t.f4_depth = value;
-  } else if (!strcmp(key, "gemv_long_kc")) {
-    if (value != 0 && value != 2 && value != 4)
-      return fail(DB_ERR_INVALID, "db_tune: gemv_long_kc must be 0, 2 or 4");
-    t.gemv_long_kc = value;
-  } else if (!strcmp(key, "gemv_long_gpw")) {
-    if (value != 0 && value != 1 && value != 2 && value != 4)
-      return fail(DB_ERR_INVALID, "db_tune: gemv_long_gpw must be 0, 1, 2 or 4");
-    t.gemv_long_gpw = value;
-  } else if (!strcmp(key, "gemv_long_stage")) {
-    if (value < 0 || value > 2)
-      return fail(DB_ERR_INVALID, "db_tune: gemv_long_stage must be 0, 1 or 2");
-    t.gemv_long_stage = value;
-  } else if (!strcmp(key, "gemv_pair_min_batch")) {
-    if (value < 0 || value == 1)
-      return fail(DB_ERR_INVALID, "db_tune: gemv_pair_min_batch must be 0 (automatic) or >= 2");
-    t.gemv_pair_min_batch = value;
-  } else if (!strcmp(key, "stream_waves")) {
-    if (value != 0 && value != 1 && value != 2 && value != 4)
-      return fail(DB_ERR_INVALID, "db_tune: stream_waves must be 0, 1, 2 or 4");
-    t.stream_waves = value;
-  } else if (!strcmp(key, "gemv_pass_grid")) {
-    if (value < 0 || value % 8 != 0)
-      return fail(DB_ERR_INVALID, "db_tune: gemv_pass_grid must be 0 (automatic) or a multiple of 8");
-    t.gemv_pass_grid = value;
-  } else if (!strcmp(key, "gemv_xb")) {
-    if (value != 0 && value != 1) return fail(DB_ERR_INVALID, "db_tune: gemv_xb must be 0 or 1");
-    t.gemv_xb = value;
-  } else if (!strcmp(key, "f4_min_tiles")) {
-    if (value < 1) return fail(DB_ERR_INVALID, "db_tune: f4_min_tiles must be >= 1");
-    t.f4_min_tiles = value;
-  } else {
-    return fail(DB_ERR_INVALID, "db_tune: unknown key '%s'", key);
-  }
+  const Knob* k = find_knob(key);
+  if (!k) return fail(DB_ERR_INVALID, "db_tune: unknown key '%s'", key);
+  if (!k->valid(value)) return fail(DB_ERR_INVALID, "db_tune: %s must be %s", key, k->rule);
+  dbk::tuning().*(k->field) = k->normalise ? k->normalise(value) : value;
+  return ok();
+}
+
+int db_f4_launch_info(int B, int Hq, int Hkv, int L, int S, int* splits, int* launches) {
+  const char* fn = "db_f4_launch_info";
+  if (!splits || !launches) return fail(DB_ERR_INVALID, "%s: null output", fn);
+  if (B < 1 || Hq < 1 || Hkv < 1 || L < 1 || Hq % Hkv != 0 || S < 1 || S > 256)
+    return fail(DB_ERR_INVALID, "%s: invalid shape", fn);
+  int err = 0;
+  const int nxcc = dbk::device_xcc_count(&err);
+  if (err) return hip_status((hipError_t)err, fn);
+  const dbk::F4Plan p = dbk::f4_plan(B, Hkv, L, S, nxcc, true);
+  *splits = p.splits;
+  *launches = p.splits > 1 && !p.fused_merge ? 2 : 1;
+  return ok();
+}
+
+int db_tune_get(const char* key, int* value) {
+  if (!key || !value) return fail(DB_ERR_INVALID, "db_tune_get: null argument");
+  const Knob* k = find_knob(key);
+  if (!k) return fail(DB_ERR_INVALID, "db_tune_get: unknown key '%s'", key);
+  *value = dbk::tuning().*(k->field);
   return ok();
 }
 

@@ -9,7 +9,8 @@
 namespace dbk {
 
 // Launch geometry knobs; defaults are the tuned MI355X values.  They can be
-// changed at run time through db_tune() for launch-shape sweeps.
+// changed at run time through db_tune() for launch-shape sweeps; each host
+// thread has its own set.
 struct Tuning {
   int gemv_waves_per_cu = 0;   // 0: the default, 32 waves per CU
   int gemv_mfma_min_batch = 0; // smallest batch that takes the MFMA GEMV
@@ -18,7 +19,10 @@ struct Tuning {
   int f4_blocks_per_cu = 1;    // target F4 workgroups per CU
   int f4_min_tiles = 8;        // minimum 16-row tiles per F4 split
   int f4_waves = 0;            // waves per F4 workgroup (4 or 8; 0: auto)
-  int f4_merge = 0;            // 0: merge splits in a second launch; 1: same launch
+  int f4_merge = 0;            // split merge: 0 automatic (in the same launch where
+                               // the grid numbering allows), 1 the same, 2 second launch
+  int f4_misplace = 0;         // test hook: F4 split s acts as if off its XCD when
+                               // s % k == k - 1 (0: off)
   int f4_line = 0;             // F4 score layout: 0 auto, 1 whole-line K loads, 2 plain
   int f4_combine_groups = 0;   // split groups per F4 merge workgroup (0: auto)
   int f4_depth = 0;            // F4 tiles in flight per wave: 0 auto, 1 or 2
@@ -36,6 +40,8 @@ Tuning& tuning();
 
 // Compute units of the current device (cached per device ordinal).
 int device_cu_count(int* err);
+// XCDs (accelerator complex dies) of the current device, cached likewise.
+int device_xcc_count(int* err);
 
 enum GemvMode : int {
   kGemvPlain = 0,
@@ -82,11 +88,24 @@ hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
 // Split-KV GQA decode attention with the log-sum-exp combine in-kernel.
 size_t f4_workspace_bytes(int B, int Hq, int Hkv, int S, int D);
 int f4_choose_splits(int B, int Hkv, int L, int cu_count);
+// How a call of S splits runs: the splits actually used (never more than
+// the 16-row tiles of L), tiles per split, whether the workgroups of a
+// (batch, kv-head) pair are numbered onto one XCD, and whether the splits
+// are merged in the same launch (else in a second one).
+struct F4Plan {
+  int splits;
+  int tiles_per_split;
+  bool xcd_map;
+  bool fused_merge;
+};
+F4Plan f4_plan(int B, int Hkv, int L, int S, int nxcc, bool allow_fused_merge);
+// nxcc: the device's XCD count (the in-launch merge runs only with 8).
 // allow_fused_merge = false keeps the merge in the second launch whatever
 // db_tune("f4_merge") says, so the workspace tickets are never read.
 hipError_t launch_f4(const void* q, const void* k, const void* v, void* o,
                      void* ws, int B, int Hq, int Hkv, int L, int D, int S,
-                     float scale, hipStream_t stream, bool allow_fused_merge = true);
+                     float scale, int nxcc, hipStream_t stream,
+                     bool allow_fused_merge = true);
 
 // Bytes of the per-device scratch array behind db_f4_splitkv_noalloc.
 constexpr size_t kF4ScratchBytes = DB_F4_SCRATCH_BYTES;

@@ -10,7 +10,8 @@
 //    every K/V byte is read from HBM exactly once.  The host sizes the split
 //    count so the grid is about one workgroup per CU.
 //  * Workgroups of one pair are numbered so that they all land on the same
-//    XCD (workgroup i is dispatched to XCD i % 8).
+//    XCD (workgroups i and i + 8 run on one XCD: the dispatcher deals them
+//    out round-robin over the 8 XCDs).
 //  * A wave walks 16-row tiles of its split (tile w, w + NW, ...) with two
 //    register sets of one tile each.  With DEPTH 2 one or two tiles (8-16
 //    KB) of K and V are in flight per wave; with DEPTH 1 a wave requests its
@@ -34,22 +35,25 @@
 //    cross-lane reduction at the end.
 //  * The waves merge through LDS.  With S = 1 the workgroup writes the fp16
 //    output.  With S > 1 splits each workgroup writes an unnormalised partial
-//    (o, and the pair (m, l) per head), and the S partials of every
+//    record (o, and the pair (m, l) per head), and the S records of every
 //    (pair, head) are merged by log-sum-exp in one of two ways:
+//      - in the same launch (the default where every split of a pair is
+//        aimed at one XCD): each workgroup waits for its record stores to
+//        land in its XCD's L2, takes a ticket from its pair's line in the
+//        workspace with one atomic add that also reports its XCD, and the
+//        workgroup that draws the last ticket reads every record from that
+//        L2 (device-scope loads, which skip the CU's L1), merges, writes the
+//        output and resets the ticket.  If the tickets show a split that ran
+//        on another XCD, whose record its L2 cannot see, the merger
+//        recomputes every split of the pair first, so placement changes
+//        only the speed.  Measured on MI355X at batch 1: 9.75 against
+//        10.05 us for the second launch at L = 8192, 23.6 against 23.9 us at
+//        L = 32768.  The first version took its tickets from one shared
+//        line (1.7 us lost to contention) with write-through stores and
+//        coherent loads, and measured 2 us slower than the second launch;
 //      - in a second, small launch (f4_combine), ordered by the kernel
-//        boundary (the default);
-//      - in the same launch (db_tune "f4_merge" = 1): the partials are
-//        written with agent-coherent (sc1) stores; after waiting for them the
-//        workgroup takes a ticket from its pair's counter in the workspace
-//        with one relaxed atomic add, and the workgroup that draws the last
-//        ticket reads every partial with agent-coherent loads, merges, writes
-//        the output and resets the counter to zero.  No L2 writeback and no
-//        waiting on other workgroups is involved: the stores a ticket follows
-//        have completed at the agent's coherence point before the ticket is
-//        taken.  Its critical path holds three serial trips to that point
-//        (write-through stores, ticket, coherent loads), which measured
-//        1.9-2.4 us slower on MI355X than the launch boundary of the second
-//        launch (L = 1024 and 8192, batch 1).
+//        boundary (when a pair's splits are not aimed at one XCD, and for
+//        db_f4_splitkv_noalloc, whose scratch tickets are never read).
 //
 // The merge follows the reference's two-phase split-KV form
 // (validation/src/kernels/fused/f4.cu:160-319): per-split max m, exp-sum l
@@ -81,7 +85,8 @@ struct F4Args {
   const _Float16* k;   // [B, Hkv, L, D]
   const _Float16* v;   // [B, Hkv, L, D]
   _Float16* o;         // [B, Hq, D]
-  unsigned* ticket;    // [B * Hkv]          split tickets (zero between calls)
+  unsigned* ticket;    // [B * Hkv][kTicketWords] split ticket line per pair
+                       // (zero between calls)
   float2* ml;          // [B * Hkv, G, S]    (max, exp-sum) per split, base 2
   float* opart;        // [B * Hkv, S, G, D] unnormalised split outputs
   int fused_merge;     // 1: the last split of a pair merges in this launch
@@ -89,6 +94,7 @@ struct F4Args {
   int ntiles;          // ceil(L / 16)
   int tps;             // tiles per split
   int xcd_map;         // 1: all splits of a pair on one XCD
+  int misplace_every;  // test hook: split s reports a foreign XCD if s % k == k - 1 (0: off)
   float scale_log2;    // scale * log2(e)
 };
 
@@ -101,17 +107,24 @@ __device__ __forceinline__ float weight2(float m, float M) {
   return m == kNegInf ? 0.0f : fast_exp2(m - M);
 }
 
-// Agent-coherent accesses of the split partials (sc1 stores and loads on
-// gfx950, what relaxed agent-scope atomics compile to): a store is visible
-// device-wide once it has completed, and a load never returns a stale line
-// of another XCD's partials.  kSc1 is the sc1 cache-policy bit of a buffer
-// load.
-constexpr int kSc1 = 16;
 // s_waitcnt vmcnt(0) with the other counters left alone (gfx9 encoding).
 constexpr int kVmcnt0 = 0x0F70;
-__device__ __forceinline__ void store_coherent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+// Cache-policy bit sc1 (device scope) of a buffer load: the load always
+// misses the CU's vector L1 and reads the XCD's L2, where the other CUs'
+// record stores have landed (a workgroup-scope load may hit a stale L1
+// line).  On MI355X it costs what a plain L2 hit does (165 vs 165 ns).
+constexpr int kSc1 = 16;
+// s_getreg_b32 operand of HW_REG_XCC_ID bits [3:0]: the XCD a wave runs on.
+constexpr int kXccIdReg = (3 << 11) | 20;
+// One 256-byte line per (batch, kv-head) pair, its first 8 bytes the split
+// ticket: arrivals in bits 0-15, the sum of the arrivals' XCC ids in bits
+// 16-31 and the sum of their squares in bits 32-47; word kRecomputeWord
+// counts the merges that had to recompute the pair.  A line of its own per
+// pair: with the 8 tickets of a batch-1 call in one line, the 256 atomics of
+// a call contended for it and the in-launch merge measured 1.7 us slower
+// (12.16 vs 10.42 us at L = 8192).
+constexpr int kTicketWords = 64;
+constexpr int kRecomputeWord = 2;
 
 template <int G, int NW, bool LINE, int DEPTH>
 __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
@@ -172,14 +185,18 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
   // L = 1024: 0.2-0.4 us), and slower once larger batches stream long
   // splits (batch 4 / 8 at L = 8192: +0.2 / +1.0 us, at L = 32768: +3 us),
   // so the launcher picks by tiles per wave and pair count.
+  // q is read through a buffer resource that covers the pair's G heads
+  // only: lanes of heads >= G get zeros without a branch (with the load
+  // under a branch the compiler copied its result inside the branch and
+  // waited for it there, before the first K/V tile was requested).
   h8 qop[LINE ? 2 : 4];
+  const __amdgpu_buffer_rsrc_t r_q = make_rsrc(a.q + q_base, G * kD * (int)sizeof(_Float16));
 #pragma unroll
   for (int t = 0; t < (LINE ? 2 : 4); ++t) {
     const int head = LINE ? (n16 & 7) : n16;
     const int chunk = LINE ? 8 * t + 2 * g4 + (n16 >> 3) : g4 + 4 * t;
-    u4 raw = {0, 0, 0, 0};
-    if (head < G) raw = ld16(a.q + q_base + (size_t)head * kD + chunk * 8);
-    qop[t] = __builtin_bit_cast(h8, raw);
+    qop[t] = __builtin_bit_cast(
+        h8, __builtin_amdgcn_raw_buffer_load_b128(r_q, (head * kD + chunk * 8) * 2, 0, 0));
   }
   // Tile key held in slot j (j = 0..3) of lane group g4 after the scores:
   // 4 g4 + j for the plain layout; key_of(j) = 2 g4 + (j & 1) + 8 (j >> 1)
@@ -196,241 +213,293 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
   // select, so the DPP before it always runs with every lane enabled).
   const float lane_scale = (!LINE || n16 < 8) ? a.scale_log2 : 0.0f;
 
-  const int t_begin = split * a.tps;
-  const int t_end = min(a.ntiles, t_begin + a.tps);
-  const int first = t_begin + wave;
-  const int nt = first < t_end ? (t_end - first + NW - 1) / NW : 0;
-  // Global index of this wave's k-th tile.
-  auto tile_of = [&](int k) { return first + NW * k; };
-  const int last_row = a.L - 1;
+  // ---- one split: stream its tiles, merge the waves, write its record ----
+  // Called for the workgroup's own split, and by a merging workgroup that
+  // recomputes every split of its pair.
+  auto run_split = [&](int split) {
+    const int t_begin = split * a.tps;
+    const int t_end = min(a.ntiles, t_begin + a.tps);
+    const int first = t_begin + wave;
+    const int nt = first < t_end ? (t_end - first + NW - 1) / NW : 0;
+    // Global index of this wave's k-th tile.
+    auto tile_of = [&](int k) { return first + NW * k; };
+    const int last_row = a.L - 1;
 
-  // O^T accumulators: lane (g4, n16) holds O[head n16][16 b + 4 g4 + i].
-  f4 o[kD / 16];
+    // O^T accumulators: lane (g4, n16) holds O[head n16][16 b + 4 g4 + i].
+    f4 o[kD / 16];
 #pragma unroll
-  for (int b = 0; b < kD / 16; ++b) o[b] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-  float m_run = kNegInf;  // per head n16 (uniform over g4)
-  float l_run = 0.0f;     // partial over this lane's keys
+    for (int b = 0; b < kD / 16; ++b) o[b] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = kNegInf;  // per head n16 (uniform over g4)
+    float l_run = 0.0f;     // partial over this lane's keys
 
-  // LINE: kt[2 kg + t] = key group kg, line t; plain: kt[t] = chunks
-  // g4 + 4t of key n16.  vt[j]: V row 4 g4 + j of the tile.
-  auto load_tile = [&](u4 (&kt)[4], u4 (&vt)[4], int tile) {
-    const int row0 = tile * kTile;
-    if constexpr (LINE) {
+    // LINE: kt[2 kg + t] = key group kg, line t; plain: kt[t] = chunks
+    // g4 + 4t of key n16.  vt[j]: V row 4 g4 + j of the tile.
+    auto load_tile = [&](u4 (&kt)[4], u4 (&vt)[4], int tile) {
+      const int row0 = tile * kTile;
+      if constexpr (LINE) {
 #pragma unroll
-      for (int kg = 0; kg < 2; ++kg) {
-        const int kr = min(row0 + 8 * kg + (n16 >> 1), last_row);
+        for (int kg = 0; kg < 2; ++kg) {
+          const int kr = min(row0 + 8 * kg + (n16 >> 1), last_row);
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-          kt[2 * kg + t] =
-              ld_stream(Kp + (size_t)kr * kD + (8 * t + 2 * g4 + (n16 & 1)) * 8);
+          for (int t = 0; t < 2; ++t)
+            kt[2 * kg + t] =
+                ld_stream(Kp + (size_t)kr * kD + (8 * t + 2 * g4 + (n16 & 1)) * 8);
+        }
+      } else {
+        const int kr = min(row0 + n16, last_row);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) kt[t] = ld_stream(Kp + (size_t)kr * kD + (g4 + 4 * t) * 8);
       }
-    } else {
-      const int kr = min(row0 + n16, last_row);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) kt[t] = ld_stream(Kp + (size_t)kr * kD + (g4 + 4 * t) * 8);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int vr = min(row0 + 4 * g4 + j, last_row);
-      vt[j] = ld_stream(Vp + (size_t)vr * kD + n16 * 8);
-    }
-  };
-
-  // V^T operands come from a per-wave row-major copy of the V tile in LDS
-  // (rows in the key order above), read back with ds_read_b64_tr_b16: lane
-  // 16g + 4r + q supplies the address of LDS row 4g + r, column d0 + 4q, and
-  // receives rows 4g .. 4g+3 of column d0 + (lane & 15) -- tile keys
-  // key_of(0..3) of lane group g -- the A-operand layout of
-  // v_mfma_f32_16x16x16_f16 for O^T = V^T P^T.
-  _Float16* vbuf = &s_v[wave][0][0];
-  auto compute_tile = [&](const u4 (&kt)[4], const u4 (&vt)[4], int tile) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      *reinterpret_cast<u4*>(vbuf + v_row(4 * g4 + j) * kVStride + 8 * n16) = vt[j];
-
-    // s[j]: scaled score of tile key key_of(j) (-inf past L).
-    float s[4];
-    if constexpr (LINE) {
-      f4 d[2];
-#pragma unroll
-      for (int kg = 0; kg < 2; ++kg) {
-        d[kg] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-          d[kg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              __builtin_bit_cast(h8, kt[2 * kg + t]), qop[t], d[kg], 0, 0, 0);
-      }
-      // key_of(j) = 8 kg + 2 g4 + r with kg = j >> 1, r = j & 1
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const f4& dk = d[j >> 1];
-        const int r = j & 1;
-        s[j] = (dk[2 * r] + dpp<kRowRor8>(dk[2 * r + 1])) * lane_scale;
+        const int vr = min(row0 + 4 * g4 + j, last_row);
+        vt[j] = ld_stream(Vp + (size_t)vr * kD + n16 * 8);
       }
-    } else {
-      f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, kt[t]), qop[t],
-                                                     acc, 0, 0, 0);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) s[j] = acc[j] * lane_scale;
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (tile * kTile + key_of(j) >= a.L) s[j] = kNegInf;
-    float tmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    tmax = fmaxf(tmax, xor_lanes(tmax, 16));
-    tmax = fmaxf(tmax, xor_lanes(tmax, 32));
-    const float m_new = fmaxf(m_run, tmax);
-    const float alpha = fast_exp2(m_run - m_new);
-    // P^T operand: lane (g4, n16) holds P[key key_of(j)][head n16] in slot
-    // j, the order the V tile was written in.  p is rounded to fp16 for the
-    // product (as the reference stage rounds p before P.V) and the exp-sum
-    // adds the rounded values, so numerator and denominator agree.
-    h4 pb;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pb[i] = (_Float16)fast_exp2(s[i] - m_new);
-    l_run = l_run * alpha + (((float)pb[0] + (float)pb[1]) + ((float)pb[2] + (float)pb[3]));
-    m_run = m_new;
+    };
 
-    // Rescale the running output only when some head's max moved; alpha of
-    // head n16 lives in the lanes that hold that head's outputs.
-    if (__any(alpha != 1.0f)) {
+    // V^T operands come from a per-wave row-major copy of the V tile in LDS
+    // (rows in the key order above), read back with ds_read_b64_tr_b16: lane
+    // 16g + 4r + q supplies the address of LDS row 4g + r, column d0 + 4q, and
+    // receives rows 4g .. 4g+3 of column d0 + (lane & 15) -- tile keys
+    // key_of(0..3) of lane group g -- the A-operand layout of
+    // v_mfma_f32_16x16x16_f16 for O^T = V^T P^T.
+    _Float16* vbuf = &s_v[wave][0][0];
+    auto compute_tile = [&](const u4 (&kt)[4], const u4 (&vt)[4], int tile) {
 #pragma unroll
-      for (int b = 0; b < kD / 16; ++b) o[b] *= alpha;
-    }
-#pragma unroll
-    for (int b = 0; b < kD / 16; ++b) {
-      const h4 va = __builtin_bit_cast(
-          h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                  (__attribute__((address_space(3))) s4*)(
-                      vbuf + (4 * g4 + (n16 >> 2)) * kVStride + 16 * b + 4 * (n16 & 3))));
-      o[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb, o[b], 0, 0, 0);
-    }
-  };
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<u4*>(vbuf + v_row(4 * g4 + j) * kVStride + 8 * n16) = vt[j];
 
-  // ---- stream this wave's tiles ------------------------------------------
-  // Two register sets of one tile each: an iteration loads set B, consumes
-  // set A, reloads A and consumes B, so one or two tiles are in flight and
-  // every wait is for one tile.  (Set B is loaded and consumed in the same
-  // iteration, which keeps the compiler from draining all loads at the loop
-  // header.)  Measured on MI355X against sets of two tiles (two to four in
-  // flight): 24.5 vs 25.0 us at batch 1, L = 32768, and 1-1.5% faster at
-  // batch 4 and 8; deeper queues per wave only spread the tiles' arrival
-  // times and lengthen the tail of the slowest wave.  DEPTH 1 (a tuning
-  // option for the 8-wave whole-line kernel) waits for the oldest tile
-  // before requesting the next, so each wave keeps one tile in flight while
-  // it computes.
-  // Timestamps of an instrumented copy there show the waves of one
-  // workgroup finishing up to 4-6 us apart; handing tiles out from an LDS
-  // counter instead of the fixed w, w + NW, ... walk (so that faster waves
-  // take more) measured slower at every shape (0.2-0.9 us), as did
-  // interleaving the splits' tiles (split s taking tiles s, s + S, ...).
-  if (nt > 0) {
-    u4 ka[4], va[4], kb[4], vb[4];
-    load_tile(ka, va, tile_of(0));
-    if constexpr (DEPTH == 1) {
-      // One tile in flight: wait for the oldest tile, request the next one,
-      // then consume the oldest.
-      for (int k = 0; k < nt; k += 2) {
-        __builtin_amdgcn_s_waitcnt(kVmcnt0);
-        if (k + 1 < nt) load_tile(kb, vb, tile_of(k + 1));
-        __builtin_amdgcn_sched_barrier(0);
-        compute_tile(ka, va, tile_of(k));
-        if (k + 1 >= nt) break;
-        __builtin_amdgcn_s_waitcnt(kVmcnt0);
-        if (k + 2 < nt) load_tile(ka, va, tile_of(k + 2));
-        __builtin_amdgcn_sched_barrier(0);
-        compute_tile(kb, vb, tile_of(k + 1));
-      }
-    } else {
-      int k = 0;
-      for (; k + 3 <= nt; k += 2) {
-        load_tile(kb, vb, tile_of(k + 1));
-        compute_tile(ka, va, tile_of(k));
-        load_tile(ka, va, tile_of(k + 2));
-        compute_tile(kb, vb, tile_of(k + 1));
-      }
-      // One or two tiles remain; set A holds tile k.  Each case is
-      // straight-line code: after a load under a branch the compiler merged
-      // the two paths and had tile k wait for tile k + 1's loads as well
-      // (vmcnt(7..0) where vmcnt(15..8) would do, read in the ISA), so at
-      // two tiles per wave nothing overlapped the second tile's arrival
-      // (batch 1, L = 8192: 10.40 -> 9.98 us; batch 8, L = 1024 10.38 ->
-      // 10.06 us).
-      if (k + 1 < nt) {
-        load_tile(kb, vb, tile_of(k + 1));
-        compute_tile(ka, va, tile_of(k));
-        compute_tile(kb, vb, tile_of(k + 1));
+      // s[j]: scaled score of tile key key_of(j) (-inf past L).
+      float s[4];
+      if constexpr (LINE) {
+        f4 d[2];
+#pragma unroll
+        for (int kg = 0; kg < 2; ++kg) {
+          d[kg] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+            d[kg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                __builtin_bit_cast(h8, kt[2 * kg + t]), qop[t], d[kg], 0, 0, 0);
+        }
+        // key_of(j) = 8 kg + 2 g4 + r with kg = j >> 1, r = j & 1
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const f4& dk = d[j >> 1];
+          const int r = j & 1;
+          s[j] = (dk[2 * r] + dpp<kRowRor8>(dk[2 * r + 1])) * lane_scale;
+        }
       } else {
-        compute_tile(ka, va, tile_of(k));
+        f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, kt[t]), qop[t],
+                                                       acc, 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s[j] = acc[j] * lane_scale;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (tile * kTile + key_of(j) >= a.L) s[j] = kNegInf;
+      float tmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+      tmax = fmaxf(tmax, xor_lanes(tmax, 16));
+      tmax = fmaxf(tmax, xor_lanes(tmax, 32));
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = fast_exp2(m_run - m_new);
+      // P^T operand: lane (g4, n16) holds P[key key_of(j)][head n16] in slot
+      // j, the order the V tile was written in.  p is rounded to fp16 for the
+      // product (as the reference stage rounds p before P.V) and the exp-sum
+      // adds the rounded values, so numerator and denominator agree.
+      h4 pb;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pb[i] = (_Float16)fast_exp2(s[i] - m_new);
+      l_run = l_run * alpha + (((float)pb[0] + (float)pb[1]) + ((float)pb[2] + (float)pb[3]));
+      m_run = m_new;
+
+      // Rescale the running output only when some head's max moved; alpha of
+      // head n16 lives in the lanes that hold that head's outputs.
+      if (__any(alpha != 1.0f)) {
+#pragma unroll
+        for (int b = 0; b < kD / 16; ++b) o[b] *= alpha;
+      }
+#pragma unroll
+      for (int b = 0; b < kD / 16; ++b) {
+        const h4 va = __builtin_bit_cast(
+            h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s4*)(
+                        vbuf + (4 * g4 + (n16 >> 2)) * kVStride + 16 * b + 4 * (n16 & 3))));
+        o[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb, o[b], 0, 0, 0);
+      }
+    };
+
+    // ---- stream this wave's tiles ------------------------------------------
+    // Two register sets of one tile each: an iteration loads set B, consumes
+    // set A, reloads A and consumes B, so one or two tiles are in flight and
+    // every wait is for one tile.  (Set B is loaded and consumed in the same
+    // iteration, which keeps the compiler from draining all loads at the loop
+    // header.)  Measured on MI355X against sets of two tiles (two to four in
+    // flight): 24.5 vs 25.0 us at batch 1, L = 32768, and 1-1.5% faster at
+    // batch 4 and 8; deeper queues per wave only spread the tiles' arrival
+    // times and lengthen the tail of the slowest wave.  DEPTH 1 (a tuning
+    // option for the 8-wave whole-line kernel) waits for the oldest tile
+    // before requesting the next, so each wave keeps one tile in flight while
+    // it computes.
+    // Timestamps of an instrumented copy there show the waves of one
+    // workgroup finishing up to 4-6 us apart; handing tiles out from an LDS
+    // counter instead of the fixed w, w + NW, ... walk (so that faster waves
+    // take more) measured slower at every shape (0.2-0.9 us), as did
+    // interleaving the splits' tiles (split s taking tiles s, s + S, ...).
+    if (nt > 0) {
+      u4 ka[4], va[4], kb[4], vb[4];
+      load_tile(ka, va, tile_of(0));
+      if constexpr (DEPTH == 1) {
+        // One tile in flight: wait for the oldest tile, request the next one,
+        // then consume the oldest.
+        for (int k = 0; k < nt; k += 2) {
+          __builtin_amdgcn_s_waitcnt(kVmcnt0);
+          if (k + 1 < nt) load_tile(kb, vb, tile_of(k + 1));
+          __builtin_amdgcn_sched_barrier(0);
+          compute_tile(ka, va, tile_of(k));
+          if (k + 1 >= nt) break;
+          __builtin_amdgcn_s_waitcnt(kVmcnt0);
+          if (k + 2 < nt) load_tile(ka, va, tile_of(k + 2));
+          __builtin_amdgcn_sched_barrier(0);
+          compute_tile(kb, vb, tile_of(k + 1));
+        }
+      } else {
+        int k = 0;
+        for (; k + 3 <= nt; k += 2) {
+          load_tile(kb, vb, tile_of(k + 1));
+          compute_tile(ka, va, tile_of(k));
+          load_tile(ka, va, tile_of(k + 2));
+          compute_tile(kb, vb, tile_of(k + 1));
+        }
+        // One or two tiles remain; set A holds tile k.  Each case is
+        // straight-line code: after a load under a branch the compiler merged
+        // the two paths and had tile k wait for tile k + 1's loads as well
+        // (vmcnt(7..0) where vmcnt(15..8) would do, read in the ISA), so at
+        // two tiles per wave nothing overlapped the second tile's arrival
+        // (batch 1, L = 8192: 10.40 -> 9.98 us; batch 8, L = 1024 10.38 ->
+        // 10.06 us).
+        if (k + 1 < nt) {
+          load_tile(kb, vb, tile_of(k + 1));
+          // Request all of tile k + 1 before waiting for tile k: left to
+          // itself the compiler issued two of its eight loads, then waited
+          // for tile k's first load (about 2 us under a full-chip stream)
+          // before requesting the other six.
+          __builtin_amdgcn_sched_barrier(0);
+          compute_tile(ka, va, tile_of(k));
+          compute_tile(kb, vb, tile_of(k + 1));
+        } else {
+          compute_tile(ka, va, tile_of(k));
+        }
       }
     }
-  }
 
-  // ---- merge the waves of the workgroup through LDS ---------------------
-  float l_tot = l_run + xor_lanes(l_run, 16);
-  l_tot += xor_lanes(l_tot, 32);
-  if (lane < G) {
-    s_m[wave][lane] = m_run;
-    s_l[wave][lane] = l_tot;
-  }
-  if (n16 < G) {
-#pragma unroll
-    for (int b = 0; b < kD / 16; ++b)
-      *reinterpret_cast<f4*>(s_o(wave, n16) + 16 * b + 4 * g4) = o[b];
-  }
-  __syncthreads();
-
-  // With S > 1 a split's partial record is its running max m_s and exp-sum
-  // l_s (base 2) and its unnormalised output o_s, all fp32.  (fp16 records
-  // of o_s / l_s, half the bytes, measured 0.45 us slower per call at
-  // batch 1, L = 8192 and 32768.)
-  for (int idx = threadIdx.x; idx < G * kD; idx += kThreads) {
-    const int h = idx / kD, d = idx % kD;
-    float M = kNegInf;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][h]);
-    float ow = 0.0f, lw = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const float e = weight2(s_m[w][h], M);
-      ow += e * s_o(w, h)[d];
-      lw += e * s_l[w][h];
+    // ---- merge the waves of the workgroup through LDS ---------------------
+    float l_tot = l_run + xor_lanes(l_run, 16);
+    l_tot += xor_lanes(l_tot, 32);
+    if (lane < G) {
+      s_m[wave][lane] = m_run;
+      s_l[wave][lane] = l_tot;
     }
-    if (a.S == 1) {
-      a.o[q_base + (size_t)h * kD + d] = to_h(ow / lw);
-    } else if (a.fused_merge) {
-      store_coherent(&a.opart[(((size_t)pair * a.S + split) * G + h) * kD + d], ow);
-      if (d == 0) {
-        float* mlp = reinterpret_cast<float*>(&a.ml[((size_t)pair * G + h) * a.S + split]);
-        store_coherent(mlp, M);
-        store_coherent(mlp + 1, lw);
+    if (n16 < G) {
+#pragma unroll
+      for (int b = 0; b < kD / 16; ++b)
+        *reinterpret_cast<f4*>(s_o(wave, n16) + 16 * b + 4 * g4) = o[b];
+    }
+    __syncthreads();
+
+    // With S > 1 a split's partial record is its running max m_s and exp-sum
+    // l_s (base 2) and its unnormalised output o_s, all fp32, written with
+    // plain stores: they land in this XCD's L2, where the in-launch merge
+    // reads them, and the kernel boundary makes them visible to the second
+    // launch otherwise.  (fp16 records of o_s / l_s, half the bytes, measured
+    // 0.45 us slower per call at batch 1, L = 8192 and 32768, with the merge
+    // in a second launch.)
+    for (int idx = threadIdx.x; idx < G * kD; idx += kThreads) {
+      const int h = idx / kD, d = idx % kD;
+      float M = kNegInf;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][h]);
+      float ow = 0.0f, lw = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float e = weight2(s_m[w][h], M);
+        ow += e * s_o(w, h)[d];
+        lw += e * s_l[w][h];
       }
-    } else {
-      a.opart[(((size_t)pair * a.S + split) * G + h) * kD + d] = ow;
-      if (d == 0) a.ml[((size_t)pair * G + h) * a.S + split] = make_float2(M, lw);
+      if (a.S == 1) {
+        a.o[q_base + (size_t)h * kD + d] = to_h(ow / lw);
+      } else {
+        a.opart[(((size_t)pair * a.S + split) * G + h) * kD + d] = ow;
+        if (d == 0) a.ml[((size_t)pair * G + h) * a.S + split] = make_float2(M, lw);
+      }
     }
-  }
+  };  // run_split
+
+  // ---- in-launch merge: the last split of the pair to arrive merges ------
+  // The merger reads the split records from its own XCD's L2, so every
+  // split must have been computed on that XCD.  The numbering aims all
+  // splits of a pair at one XCD (workgroup i and i + 8 share one: the
+  // dispatcher deals workgroups out round-robin over the 8 XCDs, starting
+  // where the previous launch stopped), and each workgroup reports where it
+  // really ran: its arrival adds (1, x, x^2) for its hardware XCC id x to
+  // the pair's 64-bit ticket.  The last of S arrivals, on XCD m, finds
+  // sum x = S m and sum x^2 = S m^2 exactly when every x equals m
+  // (Cauchy-Schwarz holds with equality only for equal terms).  Otherwise
+  // it recomputes every split of the pair itself before merging, so results
+  // never depend on where a workgroup runs; only speed does.
+  // (Read after the split's stream: any scalar work placed before it delays
+  // the first tile loads.)
+  run_split(split);
   if (a.S == 1 || !a.fused_merge) return;
+  unsigned xid = __builtin_amdgcn_s_getreg(kXccIdReg);
+  if (a.misplace_every > 0 && split % a.misplace_every == a.misplace_every - 1)
+    xid ^= 8u | (unsigned)(split & 7);  // test hook: report a foreign XCD
+  __shared__ unsigned long long s_tk;
+  unsigned long long* const tk =
+      reinterpret_cast<unsigned long long*>(a.ticket + (size_t)pair * kTicketWords);
 
-  // ---- ticket: the last split of the pair to finish merges ---------------
-  __shared__ unsigned s_last;
-  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
+  // Release: every thread's record stores have completed (reached this XCD's
+  // L2) before the ticket is taken.
+  __builtin_amdgcn_s_waitcnt(kVmcnt0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    const unsigned t = __hip_atomic_fetch_add(&a.ticket[pair], 1u, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (t == (unsigned)(a.S - 1)) ? 1u : 0u;
+    const unsigned long long inc =
+        1ull | ((unsigned long long)xid << 16) | ((unsigned long long)(xid * xid) << 32);
+    s_tk = __hip_atomic_fetch_add(tk, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + inc;
   }
   __syncthreads();
-  if (!s_last) return;
+  {
+    const unsigned long long t = s_tk;
+    const unsigned S = (unsigned)a.S;
+    if ((unsigned)(t & 0xFFFFu) != S) return;
+    if ((unsigned)((t >> 16) & 0xFFFFu) != S * xid ||
+        (unsigned)((t >> 32) & 0xFFFFu) != S * xid * xid) {
+      // Some split ran on another XCD: recompute every split of the pair
+      // here (a cold path; the fast path above stays straight-line code).
+      // Count the pair's recomputes (never reset here): a diagnostic that
+      // shows whether calls stay on the fast path.
+      if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(a.ticket + (size_t)pair * kTicketWords + kRecomputeWord, 1u,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int s = 0; s < a.S; ++s) {
+        __syncthreads();  // the previous record loop's LDS reads are done
+        run_split(s);
+      }
+      __builtin_amdgcn_s_waitcnt(kVmcnt0);  // the recomputed records are in L2
+      __syncthreads();
+    }
+  }
 
-  // Merge: thread (grp, slot) owns float4 slot `slot` of the G x D outputs
-  // and the splits grp, grp + kGrp, ...; all loads of a chunk of 8 splits are
-  // issued at once (agent-coherent 16- and 8-byte buffer loads), so S <= 8 kGrp
-  // costs one round trip.  The split groups then meet in LDS.
+  // ---- merge the S records of the pair -----------------------------------
+  // Thread (grp, slot) owns float4 slot `slot` of the G x D outputs and the
+  // splits grp, grp + kGrp, ...; the loads of a chunk of 8 splits are issued
+  // at once (16- and 8-byte buffer loads that miss the vector L1 and hit the
+  // XCD's L2), so S <= 8 kGrp costs one round trip; the split groups then
+  // meet in LDS.  (Split groups as adjacent lanes merged by lane exchanges
+  // instead, with four splits per load instruction, measured 1 us slower at
+  // batch 1, L = 8192 and 32768.)
   {
     constexpr int kSlots = G * kD / 4;
     constexpr int kGrp = kThreads / kSlots;  // >= 1: kThreads >= 256 >= kSlots
@@ -446,42 +515,40 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
         make_rsrc(a.opart + (size_t)pair * a.S * G * kD, a.S * G * kD * (int)sizeof(float));
     float M = kNegInf, Ls = 0.0f;
     f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (grp < kGrp) {
-      for (int s0 = grp; s0 < a.S; s0 += 8 * kGrp) {
-        f4 ov[8];
-        float2 mv[8];
+    for (int s0 = grp; s0 < a.S; s0 += 8 * kGrp) {
+      f4 ov[8];
+      float2 mv[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          // splits past S read zero bytes (out of the buffer's range)
-          const int sj = s0 + j * kGrp;
-          ov[j] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(
-                                             r_op, ((sj * G + h) * kD + 4 * d4) * 4, 0, kSc1));
-          mv[j] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
-                                                 r_ml, (h * a.S + sj) * 8, 0, kSc1));
-          if (sj >= a.S) mv[j].x = kNegInf;
-        }
-        float Mn = M;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) Mn = fmaxf(Mn, mv[j].x);
-        const float r = weight2(M, Mn);
-        Ls *= r;
-        acc *= r;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float w = weight2(mv[j].x, Mn);
-          Ls = fmaf(w, mv[j].y, Ls);
-          acc += w * ov[j];
-        }
-        M = Mn;
+      for (int j = 0; j < 8; ++j) {
+        // splits past S read zero bytes (out of the buffer's range)
+        const int sj = s0 + j * kGrp;
+        ov[j] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           r_op, ((sj * G + h) * kD + 4 * d4) * 4, 0, kSc1));
+        mv[j] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
+                                               r_ml, (h * a.S + sj) * 8, 0, kSc1));
+        if (sj >= a.S) mv[j].x = kNegInf;
       }
-      float* c = &s_merge[grp][slot][0];
-      c[0] = M;
-      c[1] = Ls;
-      c[2] = acc[0];
-      c[3] = acc[1];
-      c[4] = acc[2];
-      c[5] = acc[3];
+      float Mn = M;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) Mn = fmaxf(Mn, mv[j].x);
+      const float r = weight2(M, Mn);
+      Ls *= r;
+      acc *= r;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float w = weight2(mv[j].x, Mn);
+        Ls = fmaf(w, mv[j].y, Ls);
+        acc += w * ov[j];
+      }
+      M = Mn;
     }
+    float* c = &s_merge[grp][slot][0];
+    c[0] = M;
+    c[1] = Ls;
+    c[2] = acc[0];
+    c[3] = acc[1];
+    c[4] = acc[2];
+    c[5] = acc[3];
     __syncthreads();
     if (grp == 0) {
       float Mt = kNegInf;
@@ -503,8 +570,7 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
       *reinterpret_cast<uint2*>(a.o + q_base + (size_t)h * kD + (size_t)d4 * 4) = packed;
     }
   }
-  if (threadIdx.x == 0)
-    __hip_atomic_store(&a.ticket[pair], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) __hip_atomic_store(tk, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Second launch of a split call: one workgroup of kGroups x 32 threads per
@@ -619,12 +685,12 @@ int f4_max_splits(int G) {
   return 256;
 }
 
-// Workspace: [tickets: pairs x u32][ml: pairs x G x S float2][opart: pairs x
-// S x G x D fp32], the first two regions 256-byte aligned.
+// Workspace: [tickets: pairs x 256 B][ml: pairs x G x S float2][opart:
+// pairs x S x G x D fp32], the regions 256-byte aligned.
 size_t f4_workspace_bytes(int B, int Hq, int Hkv, int S, int D) {
   const int G = Hq / Hkv;
   const size_t pairs = (size_t)B * Hkv;
-  return round256(pairs * sizeof(unsigned)) + round256(pairs * G * S * sizeof(float2)) +
+  return pairs * kTicketWords * sizeof(unsigned) + round256(pairs * G * S * sizeof(float2)) +
          pairs * S * G * D * sizeof(float);
 }
 
@@ -640,11 +706,30 @@ int f4_choose_splits(int B, int Hkv, int L, int cu_count) {
   return max(S, 1);
 }
 
+F4Plan f4_plan(int B, int Hkv, int L, int S, int nxcc, bool allow_fused_merge) {
+  F4Plan p;
+  const int ntiles = (L + kTile - 1) / kTile;
+  // Never more splits than tiles: every split then owns at least one tile.
+  p.splits = min(S, ntiles);
+  p.tiles_per_split = (ntiles + p.splits - 1) / p.splits;
+  p.splits = (ntiles + p.tiles_per_split - 1) / p.tiles_per_split;
+  p.xcd_map = (B * Hkv) % 8 == 0;
+  // The in-launch merge needs the XCD-aware numbering (every split of a pair
+  // aimed at one XCD) on a device of 8 XCDs, where that numbering follows
+  // the dispatch order.  It replaces the second launch's boundary with one
+  // ticket and one L2 round trip (see f4_kernel); db_tune("f4_merge", 2)
+  // keeps the second launch.
+  p.fused_merge = allow_fused_merge && p.splits > 1 && p.xcd_map && nxcc == 8 &&
+                  tuning().f4_merge != 2;
+  return p;
+}
+
 hipError_t launch_f4(const void* q, const void* k, const void* v, void* o,
                      void* ws, int B, int Hq, int Hkv, int L, int D, int S,
-                     float scale, hipStream_t stream, bool allow_fused_merge) {
+                     float scale, int nxcc, hipStream_t stream, bool allow_fused_merge) {
   const int G = Hq / Hkv;
   const int pairs = B * Hkv;
+  const F4Plan plan = f4_plan(B, Hkv, L, S, nxcc, allow_fused_merge);
   F4Args a;
   a.q = static_cast<const _Float16*>(q);
   a.k = static_cast<const _Float16*>(k);
@@ -655,20 +740,19 @@ hipError_t launch_f4(const void* q, const void* k, const void* v, void* o,
   a.Hkv = Hkv;
   a.L = L;
   a.ntiles = (L + kTile - 1) / kTile;
-  // Never more splits than tiles: every split then owns at least one tile.
-  a.S = min(S, a.ntiles);
-  a.tps = (a.ntiles + a.S - 1) / a.S;
-  a.S = (a.ntiles + a.tps - 1) / a.tps;
+  a.S = plan.splits;
+  a.tps = plan.tiles_per_split;
   // The partial areas are laid out for the caller's S (the size it
   // allocated); the kernels use the first a.S <= S records of each pair.
   char* base = static_cast<char*>(ws);
-  const size_t ticket_bytes = round256((size_t)pairs * sizeof(unsigned));
+  const size_t ticket_bytes = (size_t)pairs * kTicketWords * sizeof(unsigned);
   const size_t ml_bytes = round256((size_t)pairs * G * S * sizeof(float2));
   a.ticket = reinterpret_cast<unsigned*>(base);
   a.ml = base ? reinterpret_cast<float2*>(base + ticket_bytes) : nullptr;
   a.opart = base ? reinterpret_cast<float*>(base + ticket_bytes + ml_bytes) : nullptr;
-  a.fused_merge = allow_fused_merge ? tuning().f4_merge : 0;
-  a.xcd_map = (pairs % 8 == 0) ? 1 : 0;
+  a.xcd_map = plan.xcd_map ? 1 : 0;
+  a.fused_merge = plan.fused_merge ? 1 : 0;
+  a.misplace_every = tuning().f4_misplace;
   a.scale_log2 = scale * kLog2e;
   (void)D;
   // 8 waves once a split has a tile for each (measured: 10% faster than 4

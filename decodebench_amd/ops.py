@@ -35,7 +35,6 @@ _lib = None
 _cu_cache: dict[int, int] = {}
 _ws_cache: dict[tuple, object] = {}
 _captured_ws: dict[tuple, object] = {}  # workspaces made under graph capture (kept alive)
-_tuned: dict[str, int] = {}      # db_tune values set through tune()
 
 _p = C.c_void_p
 _i = C.c_int
@@ -74,6 +73,8 @@ def load_library():
             "db_stream_read": (_i, [_p, C.c_size_t, _i, C.c_uint, _p, _p]),
             "db_stream_capture_id": (_i, [_p, C.POINTER(C.c_ulonglong)]),
             "db_tune": (_i, [C.c_char_p, _i]),
+            "db_tune_get": (_i, [C.c_char_p, C.POINTER(_i)]),
+            "db_f4_launch_info": (_i, [_i, _i, _i, _i, _i, C.POINTER(_i), C.POINTER(_i)]),
             "db_null_kernel": (_i, [_p]),
         }
         for name, (res, args) in protos.items():
@@ -217,9 +218,27 @@ def stream_read(src, kb_per_wave: int = 8, sink=None) -> None:
 
 
 def tune(key: str, value: int) -> None:
-    """Set a launch-geometry knob of the library (for tuning sweeps)."""
+    """Set a launch-geometry knob of the library (for tuning sweeps).  The
+    library keeps one set of knobs per host thread: the value applies to
+    the launches this thread makes."""
     _check(load_library().db_tune(key.encode(), int(value)), "db_tune")
-    _tuned[key] = int(value)
+
+
+def f4_launch_info(B: int, Hq: int, Hkv: int, L: int, S: int) -> tuple[int, int]:
+    """(splits, launches) of an F4 call of this shape on the current device:
+    launches is 1 when the split merge runs in the same launch (or there is
+    one split), 2 when it takes a second launch."""
+    s, n = C.c_int(0), C.c_int(0)
+    _check(load_library().db_f4_launch_info(B, Hq, Hkv, L, S, C.byref(s), C.byref(n)),
+           "db_f4_launch_info")
+    return s.value, n.value
+
+
+def tuned(key: str) -> int:
+    """This thread's current value of a launch-geometry knob."""
+    v = C.c_int(0)
+    _check(load_library().db_tune_get(key.encode(), C.byref(v)), "db_tune_get")
+    return v.value
 
 
 def _weights(W, w_scale, name: str, N: int, K: int):
@@ -335,26 +354,27 @@ def f4_default_splits(B: int, Hkv: int, L: int, device=None) -> int:
 
 
 def f4_workspace(B: int, Hq: int, Hkv: int, L: int, D: int, S: int, device):
-    """Workspace for db_f4_splitkv (None when S = 1).
+    """Workspace for db_f4_splitkv (None when S = 1), zero-filled when it is
+    made: the split tickets of the in-launch merge must start at zero, and
+    every call leaves them at zero again.
 
-    Outside graph capture it is cached per size, device and current stream
-    and zero-filled once, when allocated: every call leaves its split
-    tickets at zero again, so one buffer serves every later call of that
-    size on that stream, whose calls run in order.  Calls on different
-    streams get different buffers, so they may overlap.  torch draws streams
-    from a fixed pool per device, so the cache stays bounded.
+    Outside graph capture it is cached per size, device and current stream,
+    so one buffer serves every later call of that size on that stream, whose
+    calls run in order.  Calls on different streams get different buffers,
+    so they may overlap.  torch draws streams from a fixed pool per device,
+    so the cache stays bounded.
 
     Under graph capture each capture (each hipGraph being recorded) gets a
     workspace of its own from the graph's memory pool, shared by the calls
     of that size it records (they run in stream order on replay), never the
     cached one: graphs captured on torch's one capture stream would
     otherwise share it, and replaying two of them at once on different
-    streams would mix their partial records.  Those workspaces stay
-    referenced until :func:`release_captured_workspaces`, so the pool never
-    hands their memory to another graph while one that uses it can still be
-    replayed.  They are zero-filled only when the in-launch merge
-    (``tune("f4_merge", 1)``), the one reader of the tickets, is on;
-    otherwise nothing is recorded into the graph besides the F4 launches."""
+    streams would mix their partial records.  Its zero fill is recorded
+    into the graph ahead of the first F4 call of the capture, so a graph
+    replays one small fill kernel besides its F4 launches.  Those
+    workspaces stay referenced until :func:`release_captured_workspaces`,
+    so the pool never hands their memory to another graph while one that
+    uses it can still be replayed."""
     import torch
 
     nbytes = int(load_library().db_f4_workspace_bytes(B, Hq, Hkv, L, D, S))
@@ -367,18 +387,15 @@ def f4_workspace(B: int, Hq: int, Hkv: int, L: int, D: int, S: int, device):
         cid = C.c_ulonglong(0)
         _check(load_library().db_stream_capture_id(stream, C.byref(cid)),
                "db_stream_capture_id")
-        key = (idx, stream, cid.value, nbytes, _tuned.get("f4_merge", 0))
-        ws = _captured_ws.get(key)
-        if ws is None:
-            make = torch.zeros if _tuned.get("f4_merge", 0) else torch.empty
-            ws = make(nbytes, dtype=torch.uint8, device=dev)
-            _captured_ws[key] = ws
-        return ws
-    key = (idx, stream, nbytes)
-    ws = _ws_cache.get(key)
+        key = (idx, stream, cid.value, nbytes)
+        cache = _captured_ws
+    else:
+        key = (idx, stream, nbytes)
+        cache = _ws_cache
+    ws = cache.get(key)
     if ws is None:
         ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
-        _ws_cache[key] = ws
+        cache[key] = ws
     return ws
 
 

@@ -114,19 +114,28 @@ int db_gemv(const void* x, const void* W, const float* w_scale, void* y,
 int db_f4_default_splits(int B, int Hkv, int L, int cu_count);
 
 /* Bytes of caller-owned workspace db_f4_splitkv needs for S splits (0 when
- * S == 1): one split ticket per (batch, kv-head) pair, then the per-split
- * partial records.  The workspace must be zero-filled before its first use;
- * every call leaves the tickets at zero again, so a workspace is zeroed once
- * and then reused by any number of calls (including graph replays). */
+ * S == 1): one 256-byte split-ticket line per (batch, kv-head) pair, then the
+ * per-split partial records.  The workspace must be zero-filled before its
+ * first use; every call leaves the tickets (the first 8 bytes of each line)
+ * at zero again, so a workspace is zeroed once and then reused by any number
+ * of calls (including graph replays).  Bytes 8-11 of a pair's line count the
+ * in-launch merges that found the pair's splits on different XCDs and
+ * recomputed them (a diagnostic; the library never resets it).  Calls that
+ * overlap in time (concurrent streams, concurrently replayed graphs) need
+ * workspaces of their own. */
 size_t db_f4_workspace_bytes(int B, int Hq, int Hkv, int L, int D, int S);
 
 /* F4: o[b,h,:] = softmax(scale * q[b,h,:] . K[b,h/G,:,:]^T) . V[b,h/G,:,:]
  * for G = Hq / Hkv query heads per KV head (grouped-query attention), fp32
  * softmax and accumulation, fp16 output.  The KV length is cut into S splits
  * whose partial (max, exp-sum, unnormalised output) records go to the
- * workspace; a second launch on the same stream merges them by log-sum-exp
- * (one launch in total when S == 1; db_tune "f4_merge" = 1 lets the last
- * split of each pair merge in the first launch instead).
+ * workspace and are merged by log-sum-exp: by the last split of each
+ * (batch, kv-head) pair to finish, in the same launch, when B * Hkv is a
+ * multiple of 8 on a device of 8 XCDs (the launch then aims every split of a
+ * pair at one XCD and the merge reads the records from that XCD's L2; if
+ * the workgroups of a pair report different XCDs, the merger recomputes
+ * every split of the pair, so the result never depends on placement);
+ * otherwise in a second launch on the same stream.  One launch when S == 1.
  * Replaces f4_partial_kernel + f4_reduce_kernel
  * (validation/src/kernels/fused/f4.cu:173-319) and the reference stages
  * scores, softmax, weighted_v (src/decodebench/demos/llama_decode.py:120-134).
@@ -144,8 +153,8 @@ int db_f4_splitkv(const void* q, const void* k, const void* v, void* o,
  * computation and kernels as db_f4_splitkv, with the split partial records
  * kept in a library-owned device array of DB_F4_SCRATCH_BYTES (4 MiB) per
  * GPU, held from the first call on that GPU until the process ends.  The
- * split merge always runs in the second launch (db_tune "f4_merge" is
- * ignored), so nothing in the array has to start at zero.
+ * split merge always runs in the second launch, so nothing in the array has
+ * to start at zero (its ticket lines are never read).
  * No counterpart in the reference: it is for callers that cannot allocate
  * device memory (code under hipGraph capture that must not call hipMalloc,
  * tight serving loops, harnesses that forbid allocation).  It calls no
@@ -195,30 +204,6 @@ int db_null_kernel(void* stream);
 int db_stream_read(const void* src, size_t bytes, int kb_per_wave, unsigned magic,
                    unsigned* sink, void* stream);
 
-/* Launch-geometry knobs for tuning sweeps: "gemv_waves_per_cu" (<= 0: the
- * default, 32), "gemv_mfma_min_batch" (0: automatic, 3 rows; 2 for the
- * e4m3 norm and gate/up modes and for plain rows longer than 4096),
- * "f4_blocks_per_cu", "f4_min_tiles",
- * "f4_waves" (4 or 8 waves per workgroup, 0: automatic), "f4_merge" (0: the
- * split merge runs in a second launch, the default; 1: in the same launch)
- * "f4_line" (F4 score-operand layout: 0 automatic, 1 whole-line K loads,
- * 2 16 keys x 64 bytes per load), "f4_combine_groups" (split groups of
- * 32 threads per merge workgroup: 1, 2, 4 or 8; 0 automatic), "f4_depth"
- * (tiles in flight per wave of the 8-wave whole-line F4 kernel: 1 or 2; 0
- * automatic), "gemv_long_kc" (k-steps of 32 columns per chunk of the
- * MFMA GEMVs that stream their activations -- plain rows longer than 4096
- * and the gate/up pair from 17 batch rows: 2 or 4; 0 automatic),
- * "gemv_long_gpw" (8-row groups per workgroup of the long-row kernel: 1, 2
- * or 4; 0 automatic), "gemv_long_stage" (its activations: 1 loaded as B
- * operands, 2 staged through LDS; 0 automatic), "gemv_pair_min_batch"
- * (batch rows from which the gate/up pair streams its activations; 0
- * automatic, 17), "stream_waves" (db_stream_read's waves per workgroup:
- * 1, 2 or 4; 0 is 4), "gemv_pass_grid" (one weight matrix above 16 batch
- * rows on MFMA: workgroups per 16-row pass, a multiple of 8; 0 automatic,
- * CUs / passes) and "gemv_xb" (1: 32-row passes with rows 16..31 of the
- * activations in LDS on the full grid instead; 0, the default, off).
- * Process-wide; no counterpart in the reference. */
-int db_tune(const char* key, int value);
 
 #ifdef __cplusplus
 }

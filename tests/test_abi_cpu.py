@@ -1,7 +1,7 @@
 """C ABI checks that need no GPU.
 
 * libdecodebench_hip.so loads and exports every function declared in
-  include/decodebench_hip.h;
+  include/*.h (the drop-in surface and the tuning hooks);
 * every contract violation returns DB_ERR_INVALID with a message before any
   HIP call (so these run on a GPU-less host);
 * the Python wrappers turn those codes into ValueError / NotImplementedError.
@@ -14,7 +14,7 @@ from pathlib import Path
 import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
-HEADER = ROOT / "include" / "decodebench_hip.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 
 
 @pytest.fixture(scope="module")
@@ -27,7 +27,7 @@ def lib():
 
 
 def declared_functions():
-    text = HEADER.read_text()
+    text = "\n".join(h.read_text() for h in HEADERS)
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(db_\w+)\s*\(", text)))
 
@@ -38,7 +38,7 @@ def test_header_declares_the_entry_points():
                  "db_f2_gateup_swiglu", "db_f2_rmsnorm_gateup_swiglu", "db_gemv",
                  "db_f4_splitkv",
                  "db_f4_workspace_bytes", "db_f4_default_splits", "db_device_cu_count",
-                 "db_f4_splitkv_noalloc", "db_tune"):
+                 "db_f4_splitkv_noalloc", "db_tune", "db_tune_get"):
         assert want in names
 
 
@@ -156,7 +156,7 @@ def test_f4_noalloc_contract_errors(lib):
 def test_f4_workspace_and_split_policy(lib):
     assert lib.db_f4_workspace_bytes(1, 32, 8, 8192, 128, 1) == 0
     ws = lib.db_f4_workspace_bytes(1, 32, 8, 8192, 128, 64)
-    assert ws >= 8 * 4 + 8 * 64 * 4 * 130 * 4      # tickets; o, m, l per (pair, split, head)
+    assert ws >= 8 * 256 + 8 * 64 * 4 * 130 * 4    # ticket lines; o, m, l per (pair, split, head)
     s = lib.db_f4_default_splits(1, 8, 8192, 256)
     assert 1 <= s <= 256
     assert lib.db_f4_default_splits(1, 8, 16, 256) == 1       # one tile -> one split
@@ -167,7 +167,8 @@ def test_tune_keys(lib):
     assert lib.db_tune(b"nope", 1) == -1
     assert lib.db_tune(b"f4_blocks_per_cu", 0) == -1
     assert lib.db_tune(b"f4_waves", 5) == -1
-    assert lib.db_tune(b"f4_merge", 2) == -1
+    assert lib.db_tune(b"f4_merge", 3) == -1
+    assert lib.db_tune(b"f4_misplace", -1) == -1
     assert lib.db_tune(b"f4_depth", 3) == -1
     assert lib.db_tune(b"f4_depth", 0) == 0
     assert lib.db_tune(b"f4_waves", 16) == -1
@@ -186,9 +187,43 @@ def test_tune_keys(lib):
     assert lib.db_tune(b"gemv_pass_grid", 0) == 0
     assert lib.db_tune(b"gemv_xb", 2) == -1
     assert lib.db_tune(b"gemv_xb", 0) == 0
+    assert lib.db_tune(b"f4_merge", 2) == 0
     assert lib.db_tune(b"f4_merge", 0) == 0
     assert lib.db_tune(b"f4_blocks_per_cu", 2) == 0
     assert lib.db_tune(b"f4_blocks_per_cu", 1) == 0   # back to the default
+
+
+def test_tune_get_reads_this_threads_knobs(lib):
+    import threading
+
+    v = C.c_int(-1)
+    assert lib.db_tune_get(b"nope", C.byref(v)) == -1 and "unknown" in last(lib)
+    assert lib.db_tune_get(b"f4_min_tiles", None) == -1
+    assert lib.db_tune_get(b"f4_min_tiles", C.byref(v)) == 0 and v.value == 8
+    # a rejected value changes nothing
+    assert lib.db_tune(b"f4_min_tiles", 0) == -1
+    assert lib.db_tune_get(b"f4_min_tiles", C.byref(v)) == 0 and v.value == 8
+    # gemv_waves_per_cu stores non-positive values as 0 (the default)
+    assert lib.db_tune(b"gemv_waves_per_cu", -3) == 0
+    assert lib.db_tune_get(b"gemv_waves_per_cu", C.byref(v)) == 0 and v.value == 0
+    seen = {}
+    try:
+        assert lib.db_tune(b"f4_merge", 2) == 0
+
+        def other():
+            w = C.c_int(-1)
+            seen["rc"] = lib.db_tune_get(b"f4_merge", C.byref(w))
+            seen["value"] = w.value
+            seen["set"] = lib.db_tune(b"f4_min_tiles", 3)
+
+        t = threading.Thread(target=other)
+        t.start()
+        t.join()
+        assert seen == {"rc": 0, "value": 0, "set": 0}   # a new thread starts from defaults
+        assert lib.db_tune_get(b"f4_merge", C.byref(v)) == 0 and v.value == 2
+        assert lib.db_tune_get(b"f4_min_tiles", C.byref(v)) == 0 and v.value == 8
+    finally:
+        assert lib.db_tune(b"f4_merge", 0) == 0
 
 
 def test_python_wrappers_check_fp8_scales():

@@ -628,11 +628,12 @@ def test_f4_score_layouts(B, Hq, Hkv, L, S):
     assert rel_l2(outs[0], outs[1]) < 2e-3
 
 
-# Shapes of the 8-wave whole-line kernel (at most 8 (batch, kv-head) pairs) run with one
-# and with two tiles in flight per wave (db_tune "f4_depth"): 8 tiles per wave (config 4,
-# L = 32768), 2, 3-4 with a partial last tile, 5-6, and 1-2 tiles.
+# Shapes of the 8-wave whole-line kernel (at least 8 tiles per split, at most 8 (batch,
+# kv-head) pairs; "f4_depth" applies to that kernel only) run with one and with two tiles
+# in flight per wave: 8 tiles per wave (config 4, L = 32768), 2, 3-4 with a partial last
+# tile, 5-6, 2-3 with G = 1, and 39-40.
 F4_DEPTH_CASES = [(1, 32, 8, 32768, None), (1, 32, 8, 8192, None), (1, 32, 8, 391, 1),
-                  (1, 32, 8, 720, 1), (1, 8, 8, 300, 3), (1, 16, 4, 5000, 2)]
+                  (1, 32, 8, 720, 1), (1, 8, 8, 300, 1), (1, 16, 4, 5000, 1)]
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,L,S", F4_DEPTH_CASES)
@@ -696,12 +697,12 @@ def test_f4_workspace_reuse_is_deterministic():
     (and a different split count on the same workspace, whose stale records
     must not leak into the result) give bitwise-identical results; partial
     records full of garbage (NaN bytes) before the first call change nothing;
-    every call leaves the split tickets at zero."""
+    every call leaves the split ticket lines at zero."""
     q, K, V = f4_inputs(1, 32, 8, 8192, 5)
     qd, Kd, Vd = q.cuda(), K.cuda(), V.cuda()
     nbytes = ops.load_library().db_f4_workspace_bytes(1, 32, 8, 8192, 128, 64)
     ws = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device="cuda")
-    ws[:256] = 0                        # the tickets of the 8 pairs (one 256-byte region)
+    ws[:8 * 256] = 0                    # the ticket lines of the 8 pairs (256 bytes each)
     first = ops.f4_flashdecode(qd, Kd, Vd, n_splits=64, workspace=ws)
     for _ in range(20):
         again = ops.f4_flashdecode(qd, Kd, Vd, n_splits=64, workspace=ws)
@@ -711,7 +712,7 @@ def test_f4_workspace_reuse_is_deterministic():
     exact = cref.attention(q.numpy(), K.numpy(), V.numpy())
     assert rel_l2(first.float().cpu().numpy(), exact) < F4_REL_L2
     torch.cuda.synchronize()
-    assert int(ws[:256].count_nonzero()) == 0
+    assert int(ws[:8 * 256].count_nonzero()) == 0     # tickets at zero, no pair recomputed
 
 
 def test_f4_concurrent_streams_get_their_own_workspace():
@@ -741,13 +742,13 @@ def test_f4_concurrent_streams_get_their_own_workspace():
             assert torch.equal(o, ref[i])
 
 
-@pytest.mark.parametrize("merge", [0, 1])
+@pytest.mark.parametrize("merge", [2, 0])
 def test_f4_graphs_replayed_concurrently_use_their_own_workspaces(merge):
     """Two graphs captured on torch's capture stream, each holding F4 calls
     of the same shape, replayed at the same time on two streams: each
     capture has its own workspace, so both graphs give their eager
     results on every replay (with the split merge in a second launch, and
-    with the in-launch merge, whose tickets must start at zero)."""
+    with the default in-launch merge, whose tickets must start at zero)."""
     inputs = [tuple(t.cuda() for t in f4_inputs(1, 32, 8, 8192, 41 + i)) for i in range(2)]
     try:
         ops.tune("f4_merge", merge)
@@ -784,19 +785,29 @@ def test_f4_graphs_replayed_concurrently_use_their_own_workspaces(merge):
 
 @pytest.mark.parametrize("B,L", [(1, 1024), (1, 8192), (4, 8192), (8, 300)])
 def test_f4_in_launch_merge_matches_two_launch_merge(B, L):
-    """The split merge done by the last split's workgroup (f4_merge = 1) and
-    by a second launch (the default) agree to fp32 summation order, and 100
-    back-to-back calls of the in-launch merge are bitwise identical (the
-    ticket of every pair is taken exactly once per call and reset)."""
+    """The split merge done by the last split's workgroup (the default on an
+    8-XCD device when B * Hkv is a multiple of 8) and by a second launch
+    (f4_merge = 2) agree to fp32 summation order, and 100 back-to-back calls
+    of the in-launch merge are bitwise identical (the ticket of every pair is
+    taken exactly once per call and reset)."""
     print(f"[f4-merge] B={B} L={L}", flush=True)
     q, K, V = f4_inputs(B, 32, 8, L, 90 + B + L)
     qd, Kd, Vd = q.cuda(), K.cuda(), V.cuda()
     lib = ops.load_library()
-    two = ops.f4_flashdecode(qd, Kd, Vd)
+    S = ops.f4_default_splits(B, 8, L)
+    S_run = ops.f4_launch_info(B, 32, 8, L, S)[0]
+    assert ops.f4_launch_info(B, 32, 8, L, S) == (S_run, 1)   # merged in the first launch
+    ws = torch.zeros(lib.db_f4_workspace_bytes(B, 32, 8, L, 128, S), dtype=torch.uint8,
+                     device="cuda")
+    one = ops.f4_flashdecode(qd, Kd, Vd, workspace=ws)
+    outs = [ops.f4_flashdecode(qd, Kd, Vd, workspace=ws) for _ in range(100)]
+    torch.cuda.synchronize()
+    # every pair's splits ran on one XCD in all 101 calls: nothing was recomputed
+    assert int(ws[:B * 8 * 256].count_nonzero()) == 0
     try:
-        assert lib.db_tune(b"f4_merge", 1) == 0
-        one = ops.f4_flashdecode(qd, Kd, Vd)
-        outs = [ops.f4_flashdecode(qd, Kd, Vd) for _ in range(100)]
+        assert lib.db_tune(b"f4_merge", 2) == 0
+        assert ops.f4_launch_info(B, 32, 8, L, S) == (S, 2)
+        two = ops.f4_flashdecode(qd, Kd, Vd)
         torch.cuda.synchronize()
     finally:
         assert lib.db_tune(b"f4_merge", 0) == 0
@@ -805,6 +816,45 @@ def test_f4_in_launch_merge_matches_two_launch_merge(B, L):
         assert torch.equal(o, one)
     exact = cref.attention(q.numpy(), K.numpy(), V.numpy())
     assert rel_l2(one.float().cpu().numpy(), exact) < F4_REL_L2
+
+
+@pytest.mark.parametrize("B,L,k", [(1, 8192, 1), (1, 8192, 2), (1, 8192, 7), (4, 1024, 3),
+                                   (8, 300, 2), (1, 32768, 5)])
+def test_f4_misplaced_splits_are_recomputed_by_the_merger(B, L, k):
+    """In-launch merge with workgroups reporting a foreign XCD, forced from
+    the host (f4_misplace = k: split s reports another XCD when
+    s % k == k - 1; k = 1 makes every split report a different one).  The
+    merger of such a pair recomputes every split with the same code, so the
+    output is bitwise the one of a call with every workgroup in place; calls
+    after it (tickets cleared) are too."""
+    print(f"[f4-misplace] B={B} L={L} k={k}", flush=True)
+    q, K, V = f4_inputs(B, 32, 8, L, 300 + B + L + k)
+    qd, Kd, Vd = q.cuda(), K.cuda(), V.cuda()
+    S = ops.f4_default_splits(B, 8, L)
+    assert ops.f4_launch_info(B, 32, 8, L, S)[1] == 1
+    lib = ops.load_library()
+    ws = torch.zeros(lib.db_f4_workspace_bytes(B, 32, 8, L, 128, S), dtype=torch.uint8,
+                     device="cuda")
+    want = ops.f4_flashdecode(qd, Kd, Vd, workspace=ws)
+    try:
+        assert lib.db_tune(b"f4_misplace", k) == 0
+        got = [ops.f4_flashdecode(qd, Kd, Vd, workspace=ws) for _ in range(5)]
+    finally:
+        assert lib.db_tune(b"f4_misplace", 0) == 0
+    after = ops.f4_flashdecode(qd, Kd, Vd, workspace=ws)
+    torch.cuda.synchronize()
+    for o in got + [after]:
+        assert torch.equal(o, want)
+    lines = ws[:B * 8 * 256].view(torch.int32).view(B * 8, 64).cpu()
+    assert int(lines[:, :2].count_nonzero()) == 0         # tickets left at zero
+    assert int(lines[:, 3:].count_nonzero()) == 0
+    # the recompute counter: the normal calls (want, after) recomputed nothing; the
+    # forced calls recomputed every pair holding a split that reported another XCD
+    S_run = ops.f4_launch_info(B, 32, 8, L, S)[0]
+    hooked = any(s % k == k - 1 for s in range(S_run))
+    assert lines[:, 2].tolist() == [5 if hooked else 0] * (B * 8)
+    exact = cref.attention(q.numpy(), K.numpy(), V.numpy())
+    assert rel_l2(want.float().cpu().numpy(), exact) < F4_REL_L2
 
 
 def test_f4_gqa_equals_mha_on_gpu():
