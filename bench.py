@@ -78,6 +78,9 @@ def parse_args(argv=None):
     ap.add_argument("--graph", action="store_true",
                     help="with --profile-pass: replay each fused workload's calls from one "
                          "hipGraph (back-to-back launches for the kernel trace)")
+    ap.add_argument("--isolated", action="store_true",
+                    help="with --profile-pass: synchronise after every fused call, so each "
+                         "launch runs alone (its kernel-trace duration is execution time)")
     ap.add_argument("--calls", type=int, default=24,
                     help="with --profile-pass: calls per workload segment")
     ap.add_argument("--sweep-only", metavar="REGEX",
@@ -267,38 +270,50 @@ DECOMP_WORKLOADS = (("f1_cfg1", dict(name="f1")), ("f2_cfg2", dict(name="f2")),
                     ("layer_cfg5_fp8", dict(name="layer", L=8192, dtype="fp8")))
 
 
-def kernels_per_call(kw: dict) -> int:
-    """Kernel launches of one fused call (F4 with S > 1 is two launches; the
-    decode layer is F1, F4, O GEMV, RMSNorm+F2 and the down GEMV)."""
+def f4_launches(L: int, n_splits=None, batch: int = 1) -> int:
+    """Launches of one F4 call as the library plans it on this device: 1 (one
+    split, or the split merge in the same launch) or 2 (merge in a second
+    launch)."""
     from decodebench_amd import ops
+    from decodebench_amd.demos.llama_decode import LAYER
 
-    def f4_launches(L):
-        return 2 if ops.f4_default_splits(1, 8, L) > 1 else 1
+    S = ops.f4_default_splits(batch, LAYER["Hkv"], L) if n_splits is None else n_splits
+    return ops.f4_launch_info(batch, LAYER["Hq"], LAYER["Hkv"], L, S)[1]
 
+
+def kernels_per_call(kw: dict) -> int:
+    """Kernel launches of one fused call (F4 is one or two, see f4_launches;
+    the decode layer is F1, F4, O GEMV, RMSNorm+F2 and the down GEMV)."""
+    B = kw.get("batch", 1)
     if kw["name"] == "f4":
-        return f4_launches(kw.get("L", 8192)) if kw.get("n_splits") is None else \
-            (2 if kw["n_splits"] > 1 else 1)
+        return f4_launches(kw.get("L", 8192), kw.get("n_splits"), B)
     if kw["name"] == "layer":
-        return 4 + f4_launches(kw.get("L", 8192))
+        return 4 + f4_launches(kw.get("L", 8192), None, B)
     return 1
 
 
 def f4_partial_bytes(kw: dict, batch: int = 1) -> int:
     """HBM bytes a fused F4 call adds over a single-pass kernel: the split
-    partial records (o, m, l per head and split, fp32) written by the first
-    launch and read back by the merge."""
+    partial records (o, m, l per head and split, fp32).  Merged in the same
+    launch they are read back from the XCD's L2, so only their write-back
+    reaches HBM; merged by a second launch they are also read back from
+    memory."""
     from decodebench_amd import ops
     from decodebench_amd.demos.llama_decode import LAYER
 
     if kw["name"] not in ("f4", "layer"):
         return 0
     Hq, Hkv, D = LAYER["Hq"], LAYER["Hkv"], LAYER["D"]
-    S = ops.f4_default_splits(batch, Hkv, kw.get("L", 8192))
-    return 0 if S <= 1 else 2 * batch * Hq * S * (D + 2) * 4
+    L = kw.get("L", 8192)
+    S = ops.f4_default_splits(batch, Hkv, L)
+    if S <= 1:
+        return 0
+    passes = f4_launches(L, None, batch)   # 1: write only, 2: write and read
+    return passes * batch * Hq * S * (D + 2) * 4
 
 
 def profile_pass(manifest_path: str, calls: int = 24, warmup: int = 4,
-                 graph: bool = False) -> int:
+                 graph: bool = False, isolated: bool = False) -> int:
     """Launch sequence for decodebench_amd.rocprof: calibration kernels first
     (``copy_calls`` device copies of ``copy_bytes``, which read and write that
     many bytes, then ``read_calls`` launches of the read-only streaming probe
@@ -312,19 +327,25 @@ def profile_pass(manifest_path: str, calls: int = 24, warmup: int = 4,
     fused calls of a workload are captured into one hipGraph, replayed once
     as warm-up, and then replayed between the delimiters, so the kernel
     trace shows back-to-back launches with no host gaps (the unfused chains
-    stay eager)."""
+    stay eager).  ``isolated=True``: every fused call is followed by a
+    device synchronisation, so each launch runs alone on an idle GPU and the
+    kernel trace gives its execution time apart from any launch boundary
+    (the reference's single-launch timing, bench_variant.cu:441-469)."""
     import torch
 
     from decodebench_amd import ops
     from decodebench_amd.bytes_model import eliminable_bytes, total_bytes
     from decodebench_amd.demos.llama_decode import build_config
 
-    def segment(body, n):
+    def segment(body, n, sync=False):
         for i in range(2):
             body(n - 1 - i)  # warm-up, on replicas the first calls do not use first
+        torch.cuda.synchronize()
         ops.null_kernel()
         for i in range(calls):
             body(i)
+            if sync:
+                torch.cuda.synchronize()
         ops.null_kernel()
         torch.cuda.synchronize()
 
@@ -370,11 +391,12 @@ def profile_pass(manifest_path: str, calls: int = 24, warmup: int = 4,
         if graph:
             graph_segment(case)
         else:
-            segment(lambda i: case.fused(case.replicas[i % n]), n)
+            segment(lambda i: case.fused(case.replicas[i % n]), n, sync=isolated)
         workloads.append({"label": label, "kind": "fused", "calls": calls, "warmup": warmup,
                           "kernels_per_call": kernels_per_call(kw),
                           "algorithmic_bytes": case.algorithmic_bytes})
-        log(f"profile pass: {label} x {calls}" + (" (graph)" if graph else ""))
+        log(f"profile pass: {label} x {calls}" + (" (graph)" if graph else "")
+            + (" (isolated)" if isolated else ""))
         del case
         torch.cuda.empty_cache()
     for label, kw in DECOMP_WORKLOADS:
@@ -393,7 +415,7 @@ def profile_pass(manifest_path: str, calls: int = 24, warmup: int = 4,
     with open(manifest_path, "w") as f:
         json.dump({"copy_bytes": copy_bytes, "copy_calls": copy_calls,
                    "read_bytes": read_bytes, "read_calls": read_calls, "read_kb_per_wave": read_kb,
-                   "mode": "graph" if graph else "eager",
+                   "mode": "graph" if graph else ("isolated" if isolated else "eager"),
                    "delimiter": "null_kernel", "workloads": workloads}, f, indent=1)
     return 0
 
@@ -403,8 +425,8 @@ def profile_pass(manifest_path: str, calls: int = 24, warmup: int = 4,
 ROOFLINE_KERNELS = (("f1_cfg1", "gemv_kernel<1,...> (F1 RMSNorm mode)"),
                     ("f1_qkv_cfg3", "gemv_kernel<1,...> (F1 RMSNorm mode)"),
                     ("f2_cfg2", "gemv_kernel<2,...> (F2 SwiGLU mode)"),
-                    ("f4_L8192", "f4_kernel<4,8,...> + f4_combine"),
-                    ("f4_L32768", "f4_kernel<4,8,...> + f4_combine"))
+                    ("f4_L8192", "f4_kernel<4,8,...> (split merge in the same launch)"),
+                    ("f4_L32768", "f4_kernel<4,8,...> (split merge in the same launch)"))
 
 
 def load_kernel_trace(path: str) -> dict:
@@ -560,7 +582,8 @@ def main(argv=None) -> int:
     from decodebench_amd.demos.llama_decode import build_config
 
     if args.profile_pass:
-        return profile_pass(args.profile_pass, calls=args.calls, graph=args.graph)
+        return profile_pass(args.profile_pass, calls=args.calls, graph=args.graph,
+                            isolated=args.isolated)
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1

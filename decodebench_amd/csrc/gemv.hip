@@ -181,6 +181,11 @@ hipError_t launch_gemv(GemvMode mode, const void* x, const void* gamma,
   const int waves = persistent ? waves_for(a.groups, cu_count * wv)
                                : pick_waves(a.groups, cu_count);
   dim3 grid((waves + wv - 1) / wv, (B + nb - 1) / nb);
+  // F2's single-wave workgroups of one row number their row groups by XCD in
+  // 32-row slices, so each XCD writes whole output sectors: WRITE_SIZE drops
+  // from 8x its 28 KB output to about 1x.  RMSNorm -> gate/up keeps launch
+  // order (the fp16 decode layer measured 0.4 us slower with the slices).
+  a.xcd_rows = (mode == kGemvSwiGLU && wv == 1 && R == 1 && grid.x % 8 == 0) ? 1 : 0;
   hipLaunchKernelGGL(fn, grid, dim3(wv * kWave), lds, stream, a);
   return hipGetLastError();
 }

@@ -65,6 +65,8 @@ struct GemvArgs {
   int steps;              // k-steps per row group
   int kp8;                // padded activation chunks per LDS row
   int groups;             // row groups = ceil(N / R)
+  int xcd_rows;           // 1: row groups numbered so that every 32 groups of
+                          // output rows belong to one XCD (see phys below)
   float eps;
 };
 
@@ -139,6 +141,22 @@ __global__ __launch_bounds__(WV * kWave) void gemv_kernel(GemvArgs a) {
 
   const unsigned char* wmat[2] = {static_cast<const unsigned char*>(a.w0),
                                   static_cast<const unsigned char*>(a.w1)};
+  // A wave walks logical groups q = grp0, grp0 + stride_waves, ...  With
+  // xcd_rows set (single-wave workgroups of one row, a grid of a multiple of
+  // 8) every q of a workgroup has q % 8 == blockIdx.x % 8, the class of
+  // workgroups that share an XCD, and q maps to the physical group
+  //   256 (j / 32) + 32 (q % 8) + j % 32,   j = q / 8:
+  // each block of 256 rows still goes to the 256 workgroups that come up
+  // together, but its 32-row slices (64 bytes of fp16 outputs, two whole
+  // 32-byte sectors) go to one XCD each, so every output sector is written
+  // back once instead of once per XCD.  Measured on MI355X (F2, batch 1,
+  // interleaved): 33.78-33.82 us against 33.82-33.89 us for launch order;
+  // 16- and 8-row slices streamed 0.2-0.3 us slower, whole contiguous
+  // eighths of the matrix per XCD 1.5x slower (34.2 -> 51.6 us).
+  const int gspan = a.xcd_rows ? (a.groups + 255) / 256 * 256 : a.groups;
+  auto phys = [&](int q) {
+    return a.xcd_rows ? ((q >> 8) << 8) + ((q & 7) << 5) + ((q >> 3) & 31) : q;
+  };
 
   // ---- tile loader: R rows x U chunks per lane (x2 for SwiGLU), issued in
   // the order consume() uses them (chunk-major), so each wait is for the
@@ -149,8 +167,9 @@ __global__ __launch_bounds__(WV * kWave) void gemv_kernel(GemvArgs a) {
   // row scales (lane m*R + r holds the scale of matrix m, row r); a vector
   // load keeps the scalar-memory counter, which LDS reads share, clear.
   auto load_tile = [&](u4 (&dst)[NW][R][U], float& sc, int grp, int st) {
-    const bool live = grp < a.groups;
-    const int g = live ? grp : a.groups - 1;  // base stays inside the matrix
+    const int pg = phys(grp);
+    const bool live = pg < a.groups;
+    const int g = live ? pg : a.groups - 1;  // base stays inside the matrix
     const int rows = live ? min(R, a.N - g * R) : 0;
     __amdgpu_buffer_rsrc_t rs[NW];
 #pragma unroll
@@ -214,7 +233,7 @@ __global__ __launch_bounds__(WV * kWave) void gemv_kernel(GemvArgs a) {
   float wsc[2] = {0.0f, 0.0f};
   const int grp0 = blockIdx.x * kWaves + wave;
   const int ntiles =
-      grp0 < a.groups ? (a.groups - grp0 + stride_waves - 1) / stride_waves * a.steps : 0;
+      grp0 < gspan ? (gspan - grp0 + stride_waves - 1) / stride_waves * a.steps : 0;
   load_tile(wbuf[0], wsc[0], grp0, 0);
   __builtin_amdgcn_sched_barrier(0);
 
@@ -356,7 +375,7 @@ __global__ __launch_bounds__(WV * kWave) void gemv_kernel(GemvArgs a) {
     if (st == a.steps - 1) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const int row = grp * R + r;
+        const int row = phys(grp) * R + r;
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
           float out;

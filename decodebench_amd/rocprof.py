@@ -326,6 +326,29 @@ def summarize(manifest: dict, trace=None, fetch=None, write=None, raw=None) -> d
     return res
 
 
+TRAFFIC_KEYS = ("fetch_bytes", "write_bytes", "read_requests", "traffic_bytes",
+                "traffic_fetch_scaled_bytes", "traffic_over_algorithmic", "traffic_source")
+
+
+def merge_traffic(res: dict, traffic: dict) -> dict:
+    """Add the per-workload byte figures of a counter summary (``traffic``,
+    this module's JSON of the FETCH_SIZE / WRITE_SIZE / raw-request runs) to
+    a kernel-trace summary ``res``, matching workloads by label; workloads the
+    counter runs did not cover keep empty byte columns."""
+    tw = traffic.get("workloads", {})
+    for label, p in res["workloads"].items():
+        t = tw.get(label)
+        if not t:
+            continue
+        if t.get("algorithmic_bytes") != p.get("algorithmic_bytes"):
+            raise ValueError(f"{label}: algorithmic bytes {p.get('algorithmic_bytes')} in the "
+                             f"trace but {t.get('algorithmic_bytes')} in the traffic summary")
+        for k in TRAFFIC_KEYS:
+            if k in t:
+                p[k] = t[k]
+    return res
+
+
 def to_markdown(res: dict, command: str,
                 title: str = "Fused decode kernels on MI355X: duration and HBM traffic per call",
                 note: str = "") -> str:
@@ -405,6 +428,8 @@ def main(argv=None) -> int:
     ap.add_argument("--fetch")
     ap.add_argument("--write")
     ap.add_argument("--raw", help="counter CSV of a run of the raw read-request counters")
+    ap.add_argument("--traffic", help="JSON of a counter summary (--json of a FETCH_SIZE / "
+                    "WRITE_SIZE run) whose byte columns are added to this summary's workloads")
     ap.add_argument("--md")
     ap.add_argument("--json")
     ap.add_argument("--command", default="", help="command line recorded in the markdown")
@@ -417,6 +442,8 @@ def main(argv=None) -> int:
                     fetch=read_counters(args.fetch) if args.fetch else None,
                     write=read_counters(args.write) if args.write else None,
                     raw=read_counters(args.raw) if args.raw else None)
+    if args.traffic:
+        merge_traffic(res, json.loads(Path(args.traffic).read_text()))
     if args.json:
         Path(args.json).write_text(json.dumps(res, indent=1, sort_keys=True) + "\n")
     text = (to_markdown(res, args.command, args.title, args.note) if args.title

@@ -103,6 +103,10 @@ def test_f1_one_dimensional_input_and_determinism():
 # ------------------------------------------------------------------- F2
 F2_CASES = [(1, 256, 96), (2, 1024, 300), (1, 4096, 14336), (4, 4096, 14336),
             (16, 4096, 2048), (3, 4096, 1000),
+            # batch 1 with rows numbered by XCD in 32-row slices: a grid of a multiple
+            # of 8 workgroups with N not a multiple of 256 (padded row groups), and a
+            # grid that is not a multiple of 8 (launch order)
+            (1, 4096, 2000), (1, 512, 16000), (1, 4096, 1004),
             # config 2 at B = 16: two batch tiles and alternating register sets on the
             # MFMA kernel at the full gate/up shape
             (16, 4096, 14336)]

@@ -269,3 +269,26 @@ def test_traffic_uses_reads_by_size_when_the_raw_run_exists(tmp_path):
     res = rocprof.summarize(READ_MANIFEST, fetch=rd("f"), write=rd("w"))
     assert res["workloads"]["gemv"]["traffic_bytes"] == pytest.approx(15360 + 512)
     assert "FETCH_SIZE" in res["workloads"]["gemv"]["traffic_source"]
+
+
+def test_traffic_columns_merge_into_a_kernel_trace_summary():
+    """merge_traffic adds a counter run's byte columns to the trace summary
+    by workload label, and refuses a traffic file of other algorithmic bytes."""
+    from decodebench_amd import rocprof
+
+    res = {"workloads": {"f1": {"algorithmic_bytes": 100, "call_us": 1.0, "GB/s": 0.1,
+                                "kernels_per_call": 1, "kind": "fused",
+                                "kernel_us": {"gemv": 1.0}},
+                         "f4": {"algorithmic_bytes": 50, "call_us": 2.0, "GB/s": 0.025,
+                                "kernels_per_call": 1, "kind": "fused",
+                                "kernel_us": {"f4": 2.0}}}}
+    traffic = {"workloads": {"f1": {"algorithmic_bytes": 100, "write_bytes": 8.0,
+                                    "fetch_bytes": 96.0, "traffic_bytes": 104.0,
+                                    "traffic_over_algorithmic": 1.04}}}
+    rocprof.merge_traffic(res, traffic)
+    assert res["workloads"]["f1"]["traffic_over_algorithmic"] == pytest.approx(1.04)
+    assert "write_bytes" not in res["workloads"]["f4"]
+    md = rocprof.to_markdown(res, "cmd")
+    assert "| f1 |" in md and "1.040" in md
+    with pytest.raises(ValueError):
+        rocprof.merge_traffic(res, {"workloads": {"f4": {"algorithmic_bytes": 51}}})
