@@ -106,6 +106,20 @@ __device__ __forceinline__ float wave_sum(float v) {
          (lane_value(v, 32) + lane_value(v, 48));
 }
 
+// ------------------------------------------------------- LDS ordering
+// Between a wave's LDS writes and its reads of what other lanes of the same
+// wave wrote (or its reads and later overwrites): the wave's LDS accesses
+// execute in issue order, so no wait is needed, but the compiler may not
+// move a read above a write it cannot prove to touch other addresses (the
+// lanes exchange data through swizzled slots).  A wavefront-scope fence
+// pair around a wave barrier states that ordering; it emits no
+// instruction.
+__device__ __forceinline__ void wave_lds_order() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // ---------------------------------------------------------- conversions
 __device__ __forceinline__ _Float16 to_h(float f) { return (_Float16)f; }
 

@@ -268,6 +268,11 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         *reinterpret_cast<u4*>(vbuf + v_row(4 * g4 + j) * kVStride + 8 * n16) = vt[j];
+      // The transposed reads below take rows other lanes wrote here; they stay
+      // after these writes because the compiler cannot prove the lane-derived
+      // addresses disjoint (so keeps program order) and a wave's LDS accesses
+      // execute in order.  (wave_lds_order() here measured 0.13 us slower at
+      // batch 1, L = 8192: its fences also pin the global loads.)
 
       // s[j]: scaled score of tile key key_of(j) (-inf past L).
       float s[4];

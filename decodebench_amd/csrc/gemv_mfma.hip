@@ -271,12 +271,15 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
     load_gamma();
     __builtin_amdgcn_sched_barrier(0);
     put_rows(xl, 0);
+    wave_lds_order();
     get_rows(xr);
     if constexpr (XB) {
       // Rows 16..31 go to their LDS tiles, the same per-wave area, after
       // rows 0..15 have been read back (a wave's LDS accesses complete in
       // order).
+      wave_lds_order();
       put_rows(xlb, 16);
+      wave_lds_order();
       if constexpr (gemv_has_norm(MODE)) get_rows(xb);
     }
     // Without a normalisation barrier, one here keeps every wave's read-back
@@ -614,10 +617,12 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_long_kernel(MfmaArgs a) {
     if constexpr (XS) {
       // A wave's LDS accesses complete in order: the previous chunk's reads
       // are done before these writes land.
+      wave_lds_order();
 #pragma unroll
       for (int i = 0; i < kXL; ++i)
         tile[((i * kRowsPerLd) >> 3) * KC * kWave + put_base[((i * kRowsPerLd) & 7) / kRowsPerLd]] =
             xl[i];
+      wave_lds_order();
 #pragma unroll
       for (int bt = 0; bt < BT; ++bt)
 #pragma unroll
