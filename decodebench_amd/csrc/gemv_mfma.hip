@@ -32,11 +32,12 @@
 //    the last group the workgroup reduces the 8 K-slices and applies the
 //    epilogue (fp16 rounding, or SiLU(g) * u with the reference's rounding
 //    points), storing only the final fp16 outputs.
-//  * Norm modes: each wave sums x^2 over its slice, the 8 partial sums meet
-//    in LDS, and every wave normalises its own x registers as the torch
-//    stage rounds, fp16(fp16(x * inv_rms) * gamma) -- x * inv_rms rounded
-//    once rather than through fp32 (see norm_mul) -- gamma read from an LDS
-//    copy.
+//  * Norm modes: each wave sums x^2 over its slice and the 8 partial sums
+//    meet in LDS; every wave multiplies its own x registers by gamma (read
+//    from an LDS copy), fp16(x * gamma), and the epilogue scales each batch
+//    row's sums by its inv_rms: y = fp16(inv_rms * sum_k W fp16(x gamma)),
+//    so the statistic is off the path to the first product.  (32-row XB
+//    passes normalise as the torch stage rounds, see norm_mul.)
 // Batches above 16 run as passes of 16 rows (grid.y).  For one weight
 // matrix the passes of a row group run on one XCD at the same time, so the
 // later passes read its weights from L2 (see launch_gemv_mfma); 32-row
@@ -374,13 +375,32 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
     }
 #pragma unroll
     for (int bt = 0; bt < BT; ++bt) {
-      float tot = 0.0f;
+      if constexpr (XB) {
+        float tot = 0.0f;
 #pragma unroll
-      for (int v = 0; v < kWavesM; ++v) tot += red[v][8 * bt + r8];
-      const float inv = 1.0f / sqrtf(tot / (float)a.K + a.eps);
+        for (int v = 0; v < kWavesM; ++v) tot += red[v][8 * bt + r8];
+        const float inv = 1.0f / sqrtf(tot / (float)a.K + a.eps);
 #pragma unroll
-      for (int t = 0; t < KH; ++t)
-        xr[bt][t] = norm_mul(xr[bt][t], s_gamma[(FP8 ? xcol(t) : kcol + 64 * t) / 8], inv);
+        for (int t = 0; t < KH; ++t)
+          xr[bt][t] = norm_mul(xr[bt][t], s_gamma[(FP8 ? xcol(t) : kcol + 64 * t) / 8], inv);
+      } else {
+        // fp16(x * gamma), one v_pk_mul_f16 per pair; inv_rms is applied to
+        // the reduced sums in the epilogue.  Against normalising here as the
+        // stage rounds (fp16(fp16(x * inv_rms) * gamma), norm_mul) this is
+        // 0.3-0.6 us faster at 4-32 rows (F1-QKV B = 16 11.67 -> 11.26 us,
+        // B = 32 15.85 -> 15.25 us, F1 B = 32 12.1 -> 11.5 us, e4m3 F1-QKV
+        // B = 32 11.14 -> 10.6 us); the outputs move 4.4e-4 (rel-L2) from
+        // the stage and stay 4.5e-4 from the fp64 oracle.
+#pragma unroll
+        for (int t = 0; t < KH; ++t) {
+          const u4 gv = s_gamma[(FP8 ? xcol(t) : kcol + 64 * t) / 8];
+          u4 o;
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            o[q] = __builtin_bit_cast(unsigned, as_h2(xr[bt][t][q]) * as_h2(gv[q]));
+          xr[bt][t] = o;
+        }
+      }
     }
     // gamma shares the partial-sum region under XB: every wave must be done
     // with it before the first partial sum is stored.
@@ -478,6 +498,14 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
     for (int v = 0; v < kWavesM; ++v) {
       s0 += slot(jj, 0, v, n)[r];
       if constexpr (NWM == 2) s1 += slot(jj, NWM - 1, v, n)[r];
+    }
+    if constexpr (gemv_has_norm(MODE) && !XB) {
+      float tot = 0.0f;
+#pragma unroll
+      for (int v = 0; v < kWavesM; ++v) tot += red[v][n];
+      const float inv = 1.0f / sqrtf(tot / (float)a.K + a.eps);
+      s0 *= inv;
+      if constexpr (NWM == 2) s1 *= inv;
     }
     if constexpr (FP8) {
       s0 *= a.s0[row];
