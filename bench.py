@@ -35,6 +35,7 @@ the 256 MB Infinity Cache), so every step streams its weights from HBM.
 from __future__ import annotations
 
 import argparse
+import contextlib
 import json
 import math
 import os
@@ -91,6 +92,10 @@ def parse_args(argv=None):
     ap.add_argument("--kernel-trace", default=os.path.join(ROOT, "profiles",
                                                            "kernel_trace_b1.json"),
                     help="rocprofv3 graph-replay kernel-trace summary for roofline_by_kernel")
+    ap.add_argument("--kernel-trace-isolated",
+                    default=os.path.join(ROOT, "profiles", "kernel_trace_isolated_b1.json"),
+                    help="rocprofv3 kernel-trace summary of isolated launches (one call, then a "
+                         "sync) for roofline_by_kernel")
     return ap.parse_args(argv)
 
 
@@ -234,6 +239,11 @@ def sweep_workloads():
             out.append((f"f4_L{L}" + ("" if B == 1 else f"_B{B}"), dict(name="f4", L=L, batch=B)))
     for S in (1, 4, 16, 64):
         out.append((f"f4_L8192_S{S}", dict(name="f4", L=8192, batch=1, n_splits=S)))
+    # F4 with its split merge in a second launch, the form the reference times
+    # (f4_partial_kernel + f4_reduce_kernel): the fallback when a call cannot
+    # merge in its first launch
+    for L in (8192, 32768):
+        out.append((f"f4_L{L}_2launch", dict(name="f4", L=L, batch=1, tune={"f4_merge": 2})))
     # fp8 e4m3 weights (per-row scales) at batch 1, and the config-5 layer
     out += [("f1_cfg1_fp8", dict(name="f1", batch=1, dtype="fp8")),
             ("f1_qkv_cfg3_fp8", dict(name="f1_qkv", batch=1, dtype="fp8")),
@@ -251,6 +261,8 @@ def sweep_workloads():
 PROFILE_WORKLOADS = (("f1_cfg1", dict(name="f1")), ("f1_qkv_cfg3", dict(name="f1_qkv")),
                      ("f2_cfg2", dict(name="f2")), ("f4_L1024", dict(name="f4", L=1024)),
                      ("f4_L8192", dict(name="f4", L=8192)), ("f4_L32768", dict(name="f4", L=32768)),
+                     ("f4_L8192_2launch", dict(name="f4", L=8192, tune={"f4_merge": 2})),
+                     ("f4_L32768_2launch", dict(name="f4", L=32768, tune={"f4_merge": 2})),
                      ("f1_cfg1_fp8", dict(name="f1", dtype="fp8")),
                      ("f1_qkv_cfg3_fp8", dict(name="f1_qkv", dtype="fp8")),
                      ("f2_cfg2_fp8", dict(name="f2", dtype="fp8")),
@@ -268,6 +280,28 @@ DECOMP_WORKLOADS = (("f1_cfg1", dict(name="f1")), ("f2_cfg2", dict(name="f2")),
                     ("f4_L8192", dict(name="f4", L=8192)),
                     ("layer_cfg5", dict(name="layer", L=8192)),
                     ("layer_cfg5_fp8", dict(name="layer", L=8192, dtype="fp8")))
+
+
+@contextlib.contextmanager
+def knobs(kw: dict):
+    """Apply a workload's launch-geometry knobs (kw["tune"]) for the calls
+    made inside, and restore the previous values after."""
+    from decodebench_amd import ops
+
+    tune = kw.get("tune") or {}
+    old = {k: ops.tuned(k) for k in tune}
+    try:
+        for k, v in tune.items():
+            ops.tune(k, v)
+        yield
+    finally:
+        for k, v in old.items():
+            ops.tune(k, v)
+
+
+def case_args(kw: dict) -> dict:
+    """build_config arguments of a workload (its knobs removed)."""
+    return {k: v for k, v in kw.items() if k != "tune"}
 
 
 def f4_launches(L: int, n_splits=None, batch: int = 1) -> int:
@@ -386,14 +420,16 @@ def profile_pass(manifest_path: str, calls: int = 24, warmup: int = 4,
     del zeros, sink
     workloads = []
     for label, kw in PROFILE_WORKLOADS:
-        case = build_config(gen_device="cuda", **{"batch": 1, **kw})
+        case = build_config(gen_device="cuda", **{"batch": 1, **case_args(kw)})
         n = len(case.replicas)
-        if graph:
-            graph_segment(case)
-        else:
-            segment(lambda i: case.fused(case.replicas[i % n]), n, sync=isolated)
+        with knobs(kw):
+            if graph:
+                graph_segment(case)
+            else:
+                segment(lambda i: case.fused(case.replicas[i % n]), n, sync=isolated)
+            per_call = kernels_per_call(kw)
         workloads.append({"label": label, "kind": "fused", "calls": calls, "warmup": warmup,
-                          "kernels_per_call": kernels_per_call(kw),
+                          "kernels_per_call": per_call,
                           "algorithmic_bytes": case.algorithmic_bytes})
         log(f"profile pass: {label} x {calls}" + (" (graph)" if graph else "")
             + (" (isolated)" if isolated else ""))
@@ -437,13 +473,16 @@ def load_kernel_trace(path: str) -> dict:
         return {}
 
 
-def roofline_by_kernel(kernels: dict, traffic: dict, trace: dict) -> dict:
+def roofline_by_kernel(kernels: dict, traffic: dict, trace: dict, isolated: dict | None = None) -> dict:
     """Per batch-1 kernel: algorithmic bytes / its average launch time
     against 8 TB/s.  ``us`` is this run's event-timed average over
     back-to-back launches replayed from a hipGraph; ``rocprof_us`` is the
     committed rocprofv3 kernel-trace median of the same calls replayed the
-    same way (profiles/kernel_trace_b1.md, profiler overhead included);
-    ``traffic`` the committed FETCH_SIZE + WRITE_SIZE bytes per call."""
+    same way (profiles/kernel_trace_b1.md, profiler overhead included), a
+    launch-to-launch figure; ``rocprof_isolated_us`` the median duration of
+    single launches on an idle GPU (profiles/kernel_trace_isolated_b1.md),
+    the kernel's own execution time; ``traffic`` the committed read bytes by
+    request size + WRITE_SIZE per call."""
     out = {}
     for name, kernel in ROOFLINE_KERNELS:
         k = kernels.get(name)
@@ -460,6 +499,9 @@ def roofline_by_kernel(kernels: dict, traffic: dict, trace: dict) -> dict:
             row["rocprof_us"] = round(t["call_us"], 3)
             row["rocprof_kernel_us"] = {kk.split("::")[-1]: round(v, 3)
                                         for kk, v in t.get("kernel_us", {}).items()}
+        ti = (isolated or {}).get(name, {})
+        if "call_us" in ti:
+            row["rocprof_isolated_us"] = round(ti["call_us"], 3)
         out[name] = row
     return out
 
@@ -630,9 +672,10 @@ def main(argv=None) -> int:
         for name, kw in sweep_workloads():
             if args.sweep_only and not re.search(args.sweep_only, name):
                 continue
-            case = build_config(gen_device="cuda", **kw)
-            check_case(case)
-            us_k, launches = time_graph_launches(case)
+            case = build_config(gen_device="cuda", **case_args(kw))
+            with knobs(kw):
+                check_case(case)
+                us_k, launches = time_graph_launches(case)
             kernels[name] = kernel_row(case, us_k)
             kernels[name]["launches_per_graph"] = launches
             kernels[name]["traffic_bytes"] = traffic.get(name, {}).get("traffic_bytes")
@@ -641,8 +684,9 @@ def main(argv=None) -> int:
             del case
             torch.cuda.empty_cache()
         out["kernels"] = kernels
-        out["roofline_by_kernel"] = roofline_by_kernel(kernels, traffic,
-                                                       load_kernel_trace(args.kernel_trace))
+        out["roofline_by_kernel"] = roofline_by_kernel(
+            kernels, traffic, load_kernel_trace(args.kernel_trace),
+            load_kernel_trace(args.kernel_trace_isolated))
 
     if not args.quick and not args.sweep_only:
         # ---- Delta_launch vs B: unfused stream / graph vs fused ----------

@@ -292,3 +292,16 @@ def test_traffic_columns_merge_into_a_kernel_trace_summary():
     assert "| f1 |" in md and "1.040" in md
     with pytest.raises(ValueError):
         rocprof.merge_traffic(res, {"workloads": {"f4": {"algorithmic_bytes": 51}}})
+
+
+def test_a_fused_segment_counts_the_library_launches_only(tmp_path):
+    """A graph replay of fused calls also runs the fill kernel that zeroed
+    the capture's F4 workspace (once per replay): it is not part of any call,
+    so a fused segment keeps the library's dispatches only."""
+    rows = list(SEG_ROWS)
+    i = rows.index((NULL, 5, 0.0, 0.0))
+    rows.insert(i + 1, ("void at::native::vectorized_elementwise_kernel<4, FillFunctor>", 3, 0.0, 0.5))
+    trace, fetch, write = _write_rows(tmp_path, rows)
+    res = rocprof.summarize(SEG_MANIFEST, trace=trace, fetch=fetch, write=write)
+    f1 = res["workloads"]["f1"]
+    assert f1["kernels_per_call"] == 1 and f1["call_us"] == pytest.approx(3.0)
