@@ -22,7 +22,9 @@ launch on torch's current stream, so they can be used as stages and inside a
 
 from __future__ import annotations
 
+import functools
 import inspect
+import itertools
 import warnings
 from dataclasses import dataclass
 from typing import Any, Callable
@@ -241,7 +243,6 @@ class Sequence:
         """
         import torch
 
-        from decodebench_amd.graph import try_capture
         from decodebench_amd.report import Report
         from decodebench_amd.timing import time_callable
 
@@ -252,53 +253,45 @@ class Sequence:
         if fused is not None:
             self._check_fused_output(fused, replicas[0], torch)
 
-        def rotating(call):
-            state = {"i": 0}
-
-            def body():
-                r = replicas[state["i"] % len(replicas)]
-                state["i"] += 1
-                return call(r)
-            return body
-
-        stream_body = rotating(self._replay_body)
-        # Graphs of all replicas replay strictly in round-robin order, so one
-        # shared private pool holds the intermediates of every replica.
-        pool_handle = getattr(torch.cuda, "graph_pool_handle", None)
-        pool = pool_handle() if pool_handle is not None else None
-        graphs = [try_capture(lambda r=r: self._replay_body(r), pool=pool)
-                  for r in replicas]
-        failed = next((g for g in graphs if not g.ok), None)
-        if failed is not None:
-            stream_us = time_callable(stream_body, trials=trials,
+        calls = {"stream": _cycled(replicas, self._replay_body)}
+        graphs, reason = self._capture_replicas(replicas, torch)
+        if graphs is None:
+            # No graph: the report carries the stream times for both.
+            stream_us = time_callable(calls["stream"], trials=trials,
                                       target_ms=target_ms, warmup=warmup)
             return Report(self.name, stream_us, stream_us, traces,
                           byte_threshold=byte_threshold, graph_ok=False,
-                          graph_skip_reason=failed.reason)
-
-        gstate = {"i": 0}
-
-        def graph_body():
-            graphs[gstate["i"] % len(graphs)].replay()
-            gstate["i"] += 1
-
-        variants = [("stream", stream_body), ("graph", graph_body)]
+                          graph_skip_reason=reason)
+        calls["graph"] = _cycled(graphs, _replay)
         if fused is not None:
-            variants.append(("fused", rotating(fused)))
-        timings: dict[str, list[float]] = {name: [] for name, _ in variants}
-        # Rotate the variant order per round so clock or thermal drift is
-        # shared by all variants instead of biasing the last one.
-        rounds = min(3, trials)
-        for r in range(rounds):
-            n = trials // rounds + (1 if r < trials % rounds else 0)
-            k = r % len(variants)
-            for name, body in variants[k:] + variants[:k]:
-                timings[name].extend(time_callable(
-                    body, trials=n, target_ms=target_ms,
-                    warmup=warmup if r == 0 else min(warmup, 5)))
-        return Report(self.name, timings["stream"], timings["graph"], traces,
-                      fused_us=timings.get("fused"),
+            calls["fused"] = _cycled(replicas, fused)
+
+        times: dict[str, list[float]] = {name: [] for name in calls}
+        for name, n, warm in _rotation_plan(list(calls), trials, warmup):
+            times[name] += time_callable(calls[name], trials=n,
+                                         target_ms=target_ms, warmup=warm)
+        return Report(self.name, times["stream"], times["graph"], traces,
+                      fused_us=times.get("fused"),
                       byte_threshold=byte_threshold)
+
+    def _capture_replicas(self, replicas, torch):
+        """One graph of the chain per replica, or ``(None, reason)``.
+
+        All graphs record into one private memory pool: they are only ever
+        replayed one after another, so their intermediates can share it.
+        Capture stops at the first replica that fails.
+        """
+        from decodebench_amd.graph import try_capture
+
+        make_pool = getattr(torch.cuda, "graph_pool_handle", None)
+        pool = make_pool() if make_pool is not None else None
+        graphs = []
+        for rep in replicas:
+            g = try_capture(functools.partial(self._replay_body, rep), pool=pool)
+            if not g.ok:
+                return None, g.reason
+            graphs.append(g)
+        return graphs, None
 
     def _check_fused_output(self, fused, inputs, torch) -> None:
         """Fused and unfused outputs must agree elementwise (abs OR rel)."""
@@ -321,33 +314,74 @@ class Sequence:
                 "(pass requires abs < 5e-2 or rel < 2e-2 elementwise)")
 
     def _replay_body(self, inp):
-        prev = None
+        """The chain on ``inp`` with no checks: the timed stream body."""
         outputs: dict[str, Any] = {}
+        last = None
         for idx, st in enumerate(self._stages):
-            prev = st.fn(*self._bind_args(st, idx, prev, inp, outputs))
-            outputs[st.name] = prev
-        return prev
+            last = outputs[st.name] = st.fn(
+                *self._bind_args(st, idx, last, inp, outputs))
+        return last
 
     @staticmethod
     def _validate_replicas(replicas: list[dict]) -> None:
         """Every replica has replica 0's keys and tensor metadata."""
         import torch
 
-        ref = replicas[0]
+        def meta(v):
+            if not isinstance(v, torch.Tensor):
+                return (False,)
+            return (True, tuple(v.shape), v.dtype, v.stride(), v.device)
+
+        first = replicas[0]
+        want = {key: meta(v) for key, v in first.items()}
         for i, rep in enumerate(replicas[1:], start=1):
-            if set(rep) != set(ref):
+            if rep.keys() != first.keys():
                 raise ValueError(
                     f"input replica {i} keys {sorted(rep)} != replica 0 keys "
-                    f"{sorted(ref)}")
-            for key, v0 in ref.items():
+                    f"{sorted(first)}")
+            for key, expected in want.items():
                 v = rep[key]
-                is_t0, is_t = isinstance(v0, torch.Tensor), isinstance(v, torch.Tensor)
-                if is_t0 != is_t:
+                got = meta(v)
+                if got == expected:
+                    continue
+                if got[0] != expected[0]:
                     raise ValueError(
                         f"replica {i}['{key}'] tensor-ness differs from replica 0")
-                if is_t0 and (v.shape, v.dtype, v.stride(), v.device) != (
-                        v0.shape, v0.dtype, v0.stride(), v0.device):
-                    raise ValueError(
-                        f"replica {i}['{key}'] (shape={tuple(v.shape)}, "
-                        f"dtype={v.dtype}, stride={v.stride()}, device={v.device}) "
-                        "does not match replica 0")
+                raise ValueError(
+                    f"replica {i}['{key}'] (shape={tuple(v.shape)}, "
+                    f"dtype={v.dtype}, stride={v.stride()}, device={v.device}) "
+                    "does not match replica 0")
+
+
+def _cycled(items, call):
+    """A no-argument callable: the i-th invocation runs ``call(items[i % n])``."""
+    it = itertools.cycle(items)
+    return lambda: call(next(it))
+
+
+def _replay(graph):
+    graph.replay()
+
+
+def _rotation_plan(names: list[str], trials: int,
+                   warmup: int) -> list[tuple[str, int, int]]:
+    """The timing passes of ``profile``: ``(variant, trials, warmup)`` in order.
+
+    The trials of each variant are spread over up to three rounds (the first
+    ``trials % rounds`` rounds take one more).  Round ``r`` starts at variant
+    ``r mod len(names)`` and goes round the list, so slow drift in clocks or
+    temperature reaches every variant instead of biasing the one timed last.
+    The first round warms each variant up ``warmup`` calls, later rounds at
+    most 5.  This is the reference's measurement procedure
+    (src/decodebench/sequence.py:276-291).
+    """
+    rounds = min(3, trials)
+    if rounds <= 0:
+        return []
+    base, extra = divmod(trials, rounds)
+    plan = []
+    for r in range(rounds):
+        n = base + (1 if r < extra else 0)
+        warm = warmup if r == 0 else min(warmup, 5)
+        plan += [(names[(r + j) % len(names)], n, warm) for j in range(len(names))]
+    return plan

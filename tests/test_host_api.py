@@ -346,3 +346,93 @@ def test_timing_arguments_fail_before_torch_is_needed():
         time_callable(lambda: None, target_ms=math.nan)
     with pytest.raises(ValueError, match="warmup"):
         time_callable(lambda: None, warmup=-1)
+
+
+# ------------------------------------------------------- profile schedule
+def test_rotation_plan_splits_trials_and_rotates_variants():
+    """The reference's measurement procedure (sequence.py:276-291): up to
+    three rounds, the remainder to the first rounds, round r starting at
+    variant r, full warmup only in the first round."""
+    from decodebench_amd.sequence import _rotation_plan
+
+    plan = _rotation_plan(["stream", "graph", "fused"], 7, 50)
+    assert plan == [("stream", 3, 50), ("graph", 3, 50), ("fused", 3, 50),
+                    ("graph", 2, 5), ("fused", 2, 5), ("stream", 2, 5),
+                    ("fused", 2, 5), ("stream", 2, 5), ("graph", 2, 5)]
+    two = _rotation_plan(["stream", "graph"], 30, 3)
+    assert [n for _, n, _ in two] == [10] * 6
+    assert [v for v, _, _ in two] == ["stream", "graph", "graph", "stream", "stream", "graph"]
+    assert [w for _, _, w in two] == [3] * 6                 # min(3, 5) after round 0
+    assert _rotation_plan(["stream", "graph"], 2, 9) == [
+        ("stream", 1, 9), ("graph", 1, 9), ("graph", 1, 5), ("stream", 1, 5)]
+    for trials in range(1, 12):
+        plan = _rotation_plan(["a", "b", "c"], trials, 7)
+        for v in "abc":
+            assert sum(n for name, n, _ in plan if name == v) == trials
+
+
+class _FakeGraph:
+    def __init__(self, body, ok=True):
+        self.body, self.ok, self.reason = body, ok, None if ok else "capture refused"
+
+    def replay(self):
+        self.body()
+
+
+def _profile_with_fakes(monkeypatch, ok=True, fused=None, n_replicas=3):
+    """profile() on the CPU: captures and timing replaced by recorders."""
+    import torch
+
+    from decodebench_amd import graph, timing
+
+    captured, timed = [], []
+
+    def fake_capture(fn, pool=None):
+        captured.append(pool)
+        return _FakeGraph(fn, ok=ok or len(captured) < 2)
+
+    def fake_time(body, trials, target_ms, warmup):
+        for _ in range(trials):
+            body()
+        timed.append((body, trials, warmup))
+        return [float(len(timed))] * trials
+
+    monkeypatch.setattr(graph, "try_capture", fake_capture)
+    monkeypatch.setattr(timing, "time_callable", fake_time)
+    monkeypatch.setattr(torch.cuda, "graph_pool_handle", lambda: "pool")
+    seen = []
+    seq = Sequence("fake")
+
+    @seq.stage
+    def double(x):
+        seen.append(int(x[0]))
+        return x * 2
+
+    replicas = [{"x": torch.full((4,), float(i))} for i in range(n_replicas)]
+    rep = seq.profile(replicas[0], trials=7, warmup=4, input_replicas=replicas, fused=fused)
+    return rep, captured, timed, seen
+
+
+def test_profile_rotates_replicas_and_variants(monkeypatch):
+    fused_seen = []
+
+    def fused(inp):
+        fused_seen.append(int(inp["x"][0]))
+        return inp["x"] * 2
+
+    rep, captured, timed, seen = _profile_with_fakes(monkeypatch, fused=fused)
+    assert captured == ["pool"] * 3                      # one graph per replica, one pool
+    assert [(t, w) for _, t, w in timed] == [(3, 4)] * 3 + [(2, 4)] * 6
+    assert len(rep.stream_us) == len(rep.graph_us) == len(rep.fused_us) == 7
+    # trace (replica 0), the fused check (replica 0), then every timed call
+    # walks the replicas in order: stream and graph share the stage body.
+    assert seen[:2] == [0, 0] and fused_seen[0] == 0
+    assert fused_seen[1:] == [i % 3 for i in range(7)]
+
+
+def test_profile_without_graphs_reports_stream_times(monkeypatch):
+    rep, captured, timed, seen = _profile_with_fakes(monkeypatch, ok=False)
+    assert len(captured) == 2                            # stops at the failing capture
+    assert [(t, w) for _, t, w in timed] == [(7, 4)]
+    assert rep.graph_ok is False and rep.graph_skip_reason == "capture refused"
+    assert rep.stream_us == rep.graph_us
