@@ -223,11 +223,18 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   u4 xr[BT][KH];
   u4 xb[XB ? 2 : 1][KH];  // XB: rows 16..31 (norm modes: for their x^2 sums)
   u4 gchunk = {0, 0, 0, 0};
-  // F1's gamma is shared by every batch row: thread t fetches 16-byte chunk t
-  // (K / 8 <= 512 chunks) for the LDS copy the normalisation reads.
+  // gamma for the LDS copy the normalisation reads.  XB: thread t fetches
+  // 16-byte chunk t of all of gamma (K / 8 <= 512 chunks), shared by the
+  // waves; otherwise lane l of each wave fetches chunk l of the wave's own
+  // K-slice (8 KH chunks) for a wave-private copy, so no wave waits for
+  // another's before its first product.
   auto load_gamma = [&]() {
-    if constexpr (gemv_has_norm(MODE))
-      gchunk = ld16(a.gamma + 8 * min((int)threadIdx.x, a.K / 8 - 1));
+    if constexpr (gemv_has_norm(MODE)) {
+      if constexpr (XB)
+        gchunk = ld16(a.gamma + 8 * min((int)threadIdx.x, a.K / 8 - 1));
+      else
+        gchunk = ld16(a.gamma + sbase + 8 * min(lane, 8 * KH - 1));
+    }
   };
   u4 wa[NWM][KW];
   if constexpr (kStage) {
@@ -283,9 +290,9 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
       wave_lds_order();
       if constexpr (gemv_has_norm(MODE)) get_rows(xb);
     }
-    // Without a normalisation barrier, one here keeps every wave's read-back
-    // ahead of the partial sums that later share the staging area.
-    if constexpr (!XB && !gemv_has_norm(MODE)) __syncthreads();
+    // The partial sums later share the staging area: a barrier before the
+    // first partial-sum store (in consume) keeps every wave's read-back ahead
+    // of them.
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (XB && gemv_has_norm(MODE)) {
       // Rows 16..31: their x^2 sums, from the copy read back from their LDS
@@ -355,8 +362,15 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
       ss[bt] += __shfl_xor(ss[bt], 32);
       if (lane < 8) red[wave][8 * bt + lane] = ss[bt];
     }
-    if ((int)threadIdx.x < a.K / 8) s_gamma[threadIdx.x] = gchunk;
-    __syncthreads();
+    if constexpr (XB) {
+      if ((int)threadIdx.x < a.K / 8) s_gamma[threadIdx.x] = gchunk;
+      __syncthreads();
+    } else {
+      // The wave's slice of gamma (chunks sbase / 8 ..), read back by the
+      // wave's own lanes.
+      if (lane < 8 * KH) s_gamma[wave * kWave + lane] = gchunk;
+      wave_lds_order();
+    }
     if constexpr (XB) {
       // rows 16..31: normalised in place in their LDS tiles
 #pragma unroll
@@ -393,7 +407,7 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
         // the stage and stay 4.5e-4 from the fp64 oracle.
 #pragma unroll
         for (int t = 0; t < KH; ++t) {
-          const u4 gv = s_gamma[(FP8 ? xcol(t) : kcol + 64 * t) / 8];
+          const u4 gv = s_gamma[wave * kWave + ((FP8 ? xcol(t) : kcol + 64 * t) - sbase) / 8];
           u4 o;
 #pragma unroll
           for (int q = 0; q < 4; ++q)
@@ -434,6 +448,11 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
           // (g4 < 2, c16 < 8); their half-1 partners sit 40 lanes higher.
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[i] += __shfl(acc[i], lane + 40);
+          // The first partial-sum store of the workgroup: the staging area it
+          // shares must have been read back by every wave (j is uniform, and
+          // every workgroup consumes group 0 first, exactly once).
+          if constexpr (kStage && !XB)
+            if (m == 0 && bt == 0 && j == 0) __syncthreads();
           if (g4 < 2 && c16 < 8)
             *reinterpret_cast<f4*>(slot(j, m, wave, 8 * bt + c16) + 4 * g4) = acc;
         }
