@@ -103,6 +103,8 @@ struct MfmaArgs {
   int B, K, N;
   int groups;             // ceil(N / 8)
   int gpw;                // groups per workgroup (<= kMaxGroupsPerWg)
+  int part_off;           // 16-byte units from the activation staging area to the
+                          // partial sums: 0 when they share it, else past it
   float eps;
 };
 
@@ -131,7 +133,8 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   // 8 K-slice partial sums of every output of the workgroup.
   extern __shared__ __align__(16) unsigned char dyn_lds[];
   u4* xbuf = reinterpret_cast<u4*>(dyn_lds);
-  float* part = reinterpret_cast<float*>(dyn_lds + (size_t)kXbU4 * 16);
+  u4* const stage_area = reinterpret_cast<u4*>(dyn_lds + (size_t)kXbU4 * 16);
+  float* part = reinterpret_cast<float*>(stage_area + a.part_off);
   auto slot = [&](int j, int m, int v, int n) -> float* {
     return part + ((((j * NWM + m) * kWavesM + v) * kPass + n) * kRowsPerGroup);
   };
@@ -249,7 +252,7 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
     const int ch = FP8 ? (lchunk >> 3) & 1 : (lchunk >> 2) & 1;
     const int cg = FP8 ? (lchunk >> 1) & 3 : lchunk & 3;
     u4* const stage =
-        (XB ? xbuf : reinterpret_cast<u4*>(part)) + (size_t)wave * BT * KH * kWave;
+        (XB ? xbuf : stage_area) + (size_t)wave * BT * KH * kWave;
     auto load_rows = [&](u4 (&dst)[kLoads], int r0) {
 #pragma unroll
       for (int i = 0; i < kLoads; ++i) {
@@ -448,11 +451,11 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
           // (g4 < 2, c16 < 8); their half-1 partners sit 40 lanes higher.
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[i] += __shfl(acc[i], lane + 40);
-          // The first partial-sum store of the workgroup: the staging area it
+          // The first partial-sum store of the workgroup: a staging area it
           // shares must have been read back by every wave (j is uniform, and
           // every workgroup consumes group 0 first, exactly once).
           if constexpr (kStage && !XB)
-            if (m == 0 && bt == 0 && j == 0) __syncthreads();
+            if (a.part_off == 0 && m == 0 && bt == 0 && j == 0) __syncthreads();
           if (g4 < 2 && c16 < 8)
             *reinterpret_cast<f4*>(slot(j, m, wave, 8 * bt + c16) + 4 * g4) = acc;
         }
@@ -1238,6 +1241,7 @@ hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
                             const GemvWeights& w, void* y, int B, int K, int N, float eps,
                             int cu_count, hipStream_t stream) {
   MfmaArgs a;
+  a.part_off = 0;
   a.x = static_cast<const _Float16*>(x);
   a.gamma = static_cast<const _Float16*>(gamma);
   a.w0 = w.w0;
@@ -1296,7 +1300,17 @@ hipError_t launch_gemv_mfma(GemvMode mode, const void* x, const void* gamma,
   const bool staged = gemv_has_norm(mode) || (nwm == 1 && bt == 2);
   const size_t stage_bytes = staged ? (size_t)kWavesM * bt * kh * kWave * 16 : 0;
   const size_t part16 = sizeof(float) * a.gpw * nwm * kWavesM * 8 * bt * kRowsPerGroup;
-  const size_t lds = xb ? xb_bytes + part32 : (part16 > stage_bytes ? part16 : stage_bytes);
+  size_t lds = xb ? xb_bytes + part32 : (part16 > stage_bytes ? part16 : stage_bytes);
+  a.part_off = 0;
+  if (staged && !xb) {
+    // Partial sums past the staging area where both fit: then no wave waits
+    // for the others' read-back before its first partial-sum store.
+    const size_t both = stage_bytes + part16;
+    if (both <= 48 * 1024 || allow_large_lds(reinterpret_cast<const void*>(fn), both) == hipSuccess) {
+      lds = both;
+      a.part_off = (int)(stage_bytes / 16);
+    }
+  }
   if (lds > 48 * 1024) {
     hipError_t e = allow_large_lds(reinterpret_cast<const void*>(fn), lds);
     if (e != hipSuccess) return e;
