@@ -139,8 +139,9 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
     return part + ((((j * NWM + m) * kWavesM + v) * kPass + n) * kRowsPerGroup);
   };
   __shared__ float red[kWavesM][kPass];
-  // gamma's LDS copy (K / 8 chunks): static, or with XB the start of the
-  // partial-sum region, which nothing writes before the prologue ends.
+  // gamma's LDS copy: static (a K / 8-chunk slice per wave), or with XB all
+  // of gamma at the start of the partial-sum region, which nothing writes
+  // before the XB prologue's barriers.
   __shared__ u4 s_gamma_own[gemv_has_norm(MODE) && !XB ? kThreadsM : 1];
   u4* const s_gamma = XB ? reinterpret_cast<u4*>(part) : s_gamma_own;
 
@@ -218,9 +219,11 @@ __global__ __launch_bounds__(kThreadsM) void gemv_mfma_kernel(MfmaArgs a) {
   // 6.97 us, e4m3 F1 B = 8 6.40 -> 5.54 us) and RMSNorm -> gate/up at 3-16
   // rows (fp16 B = 8 37.7 -> 36.8 us, B = 16 39.8 -> 38.5 us, e4m3 B = 16
   // 23.2 -> 21.8 us).  The plain projection at one batch tile would wait for
-  // the staging barrier and does not (+0.4-0.6 us at 3-4 rows, even at 8).
-  // The staging area is the wave's XB tiles, or the partial-sum region,
-  // which nothing writes before the prologue's barrier.
+  // a staging barrier and does not (+0.4-0.6 us at 3-4 rows, even at 8).
+  // The staging area is the wave's XB tiles, or a per-wave part of the
+  // dynamic LDS that the partial sums follow (part_off) or share; when they
+  // share it, a barrier before the first partial-sum store (in consume)
+  // keeps every wave's read-back ahead of them.
   constexpr bool kStage = gemv_has_norm(MODE) || (NWM == 1 && BT == 2);
   const u4 zero4 = {0, 0, 0, 0};
   u4 xr[BT][KH];
