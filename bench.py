@@ -244,6 +244,14 @@ def sweep_workloads():
     # merge in its first launch
     for L in (8192, 32768):
         out.append((f"f4_L{L}_2launch", dict(name="f4", L=L, batch=1, tune={"f4_merge": 2})))
+    # each half of that pair alone, back to back (db_tune f4_launch): the split
+    # kernel, then the merge (reading whatever records its workspace holds, so
+    # no parity check); their times add up to the pair's
+    for L in (8192, 32768):
+        for half, only in (("split", 1), ("merge", 2)):
+            out.append((f"f4_L{L}_2launch_{half}",
+                        dict(name="f4", L=L, batch=1, tune={"f4_merge": 2, "f4_launch": only},
+                             check=False)))
     # fp8 e4m3 weights (per-row scales) at batch 1, and the config-5 layer
     out += [("f1_cfg1_fp8", dict(name="f1", batch=1, dtype="fp8")),
             ("f1_qkv_cfg3_fp8", dict(name="f1_qkv", batch=1, dtype="fp8")),
@@ -263,6 +271,14 @@ PROFILE_WORKLOADS = (("f1_cfg1", dict(name="f1")), ("f1_qkv_cfg3", dict(name="f1
                      ("f4_L8192", dict(name="f4", L=8192)), ("f4_L32768", dict(name="f4", L=32768)),
                      ("f4_L8192_2launch", dict(name="f4", L=8192, tune={"f4_merge": 2})),
                      ("f4_L32768_2launch", dict(name="f4", L=32768, tune={"f4_merge": 2})),
+                     ("f4_L8192_2launch_split",
+                      dict(name="f4", L=8192, tune={"f4_merge": 2, "f4_launch": 1}, check=False)),
+                     ("f4_L8192_2launch_merge",
+                      dict(name="f4", L=8192, tune={"f4_merge": 2, "f4_launch": 2}, check=False)),
+                     ("f4_L32768_2launch_split",
+                      dict(name="f4", L=32768, tune={"f4_merge": 2, "f4_launch": 1}, check=False)),
+                     ("f4_L32768_2launch_merge",
+                      dict(name="f4", L=32768, tune={"f4_merge": 2, "f4_launch": 2}, check=False)),
                      ("f1_cfg1_fp8", dict(name="f1", dtype="fp8")),
                      ("f1_qkv_cfg3_fp8", dict(name="f1_qkv", dtype="fp8")),
                      ("f2_cfg2_fp8", dict(name="f2", dtype="fp8")),
@@ -300,8 +316,8 @@ def knobs(kw: dict):
 
 
 def case_args(kw: dict) -> dict:
-    """build_config arguments of a workload (its knobs removed)."""
-    return {k: v for k, v in kw.items() if k != "tune"}
+    """build_config arguments of a workload (its knobs and check flag removed)."""
+    return {k: v for k, v in kw.items() if k not in ("tune", "check")}
 
 
 def f4_launches(L: int, n_splits=None, batch: int = 1) -> int:
@@ -463,6 +479,22 @@ ROOFLINE_KERNELS = (("f1_cfg1", "gemv_kernel<1,...> (F1 RMSNorm mode)"),
                     ("f2_cfg2", "gemv_kernel<2,...> (F2 SwiGLU mode)"),
                     ("f4_L8192", "f4_kernel<4,8,...> (split merge in the same launch)"),
                     ("f4_L32768", "f4_kernel<4,8,...> (split merge in the same launch)"))
+
+
+def two_launch_parts(kernels: dict) -> dict:
+    """The two-launch F4 pair against its halves timed alone back to back:
+    split kernel + merge (µs per launch) and their sum next to the pair's
+    time per call."""
+    out = {}
+    for L in (8192, 32768):
+        pair, split, merge = (kernels.get(f"f4_L{L}_2launch{sfx}")
+                              for sfx in ("", "_split", "_merge"))
+        if pair and split and merge:
+            total = split["us"] + merge["us"]
+            out[f"L{L}"] = {"split_us": split["us"], "merge_us": merge["us"],
+                            "sum_us": round(total, 3), "pair_us": pair["us"],
+                            "sum_minus_pair_us": round(total - pair["us"], 3)}
+    return out
 
 
 def load_kernel_trace(path: str) -> dict:
@@ -674,7 +706,8 @@ def main(argv=None) -> int:
                 continue
             case = build_config(gen_device="cuda", **case_args(kw))
             with knobs(kw):
-                check_case(case)
+                if kw.get("check", True):
+                    check_case(case)
                 us_k, launches = time_graph_launches(case)
             kernels[name] = kernel_row(case, us_k)
             kernels[name]["launches_per_graph"] = launches
@@ -684,6 +717,9 @@ def main(argv=None) -> int:
             del case
             torch.cuda.empty_cache()
         out["kernels"] = kernels
+        parts = two_launch_parts(kernels)
+        if parts:
+            out["f4_two_launch_parts"] = parts
         out["roofline_by_kernel"] = roofline_by_kernel(
             kernels, traffic, load_kernel_trace(args.kernel_trace),
             load_kernel_trace(args.kernel_trace_isolated))

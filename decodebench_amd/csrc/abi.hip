@@ -303,6 +303,8 @@ const Knob kKnobs[] = {
      "0 (automatic) or a multiple of 8", nullptr},
     {"gemv_xb", &dbk::Tuning::gemv_xb, [](int v) { return v == 0 || v == 1; }, "0 or 1",
      nullptr},
+    {"f4_launch", &dbk::Tuning::f4_launch, [](int v) { return v >= 0 && v <= 2; },
+     "0 (both launches), 1 (split kernel only) or 2 (merge only)", nullptr},
 };
 
 const Knob* find_knob(const char* key) {
@@ -414,7 +416,7 @@ int db_f4_launch_info(int B, int Hq, int Hkv, int L, int S, int* splits, int* la
   if (err) return hip_status((hipError_t)err, fn);
   const dbk::F4Plan p = dbk::f4_plan(B, Hkv, L, S, nxcc, true);
   *splits = p.splits;
-  *launches = p.splits > 1 && !p.fused_merge ? 2 : 1;
+  *launches = p.splits > 1 && !p.fused_merge && dbk::tuning().f4_launch == 0 ? 2 : 1;
   return ok();
 }
 

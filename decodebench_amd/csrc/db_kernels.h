@@ -35,6 +35,8 @@ struct Tuning {
                                // 16-row pass (0: CUs / passes; else a multiple of 8)
   int gemv_xb = 0;             // 1: 32-row passes (rows 16..31 of x in LDS) on the
                                // full grid instead
+  int f4_launch = 0;           // measurement hook for the two-launch F4: 0 both
+                               // launches, 1 the split kernel only, 2 the merge only
 };
 Tuning& tuning();
 

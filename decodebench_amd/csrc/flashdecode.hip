@@ -820,9 +820,14 @@ hipError_t launch_f4(const void* q, const void* k, const void* v, void* o,
   // us) and at L = 16384 (14.85 against 14.48 us), and 0.3 us slower at
   // L = 1024.
   const int depth = tuning().f4_depth > 0 ? tuning().f4_depth : 2;
-  hipLaunchKernelGGL(pick_kernel(G, waves, line, depth), dim3(pairs * a.S),
-                     dim3(waves * kWave), 0, stream, a);
-  if (a.S > 1 && !a.fused_merge) {
+  // db_tune("f4_launch", 1 or 2) launches one of the two kernels of the
+  // two-launch form alone: a measurement hook that times each half back to
+  // back (the merge alone reads whatever records the workspace holds).
+  const int only = a.S > 1 && !a.fused_merge ? tuning().f4_launch : 0;
+  if (only != 2)
+    hipLaunchKernelGGL(pick_kernel(G, waves, line, depth), dim3(pairs * a.S),
+                       dim3(waves * kWave), 0, stream, a);
+  if (a.S > 1 && !a.fused_merge && only != 1) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int forced = tuning().f4_combine_groups;

@@ -52,6 +52,12 @@ extern "C" {
  *  "gemv_xb"             (1: 32-row passes with rows 16..31 of the
  *                         activations in LDS on the full grid; 0, the default,
  *                         off)
+ *  "f4_launch"           (a call of F4 whose split merge runs in a second
+ *                         launch makes only one of its two launches: 1 the
+ *                         split kernel, 2 the merge, which then reads whatever
+ *                         records the workspace holds; 0, the default, both.
+ *                         For timing each half back to back; the output is not
+ *                         the attention result)
  * Returns DB_OK, or DB_ERR_INVALID for an unknown key or a value outside the
  * key's range (nothing changes then). */
 int db_tune(const char* key, int value);

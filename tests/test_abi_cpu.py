@@ -171,6 +171,8 @@ def test_tune_keys(lib):
     assert lib.db_tune(b"f4_misplace", -1) == -1
     assert lib.db_tune(b"f4_depth", 3) == -1
     assert lib.db_tune(b"f4_depth", 0) == 0
+    assert lib.db_tune(b"f4_launch", 3) == -1
+    assert lib.db_tune(b"f4_launch", 0) == 0
     assert lib.db_tune(b"f4_waves", 16) == -1
     assert lib.db_tune(b"gemv_long_kc", 3) == -1
     assert lib.db_tune(b"gemv_long_gpw", 3) == -1

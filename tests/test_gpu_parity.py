@@ -787,6 +787,41 @@ def test_f4_graphs_replayed_concurrently_use_their_own_workspaces(merge):
         ops.tune("f4_merge", 0)
 
 
+@pytest.mark.parametrize("L", [1024, 8192, 32768])
+def test_f4_two_launch_halves_make_the_pair(L):
+    """The measurement hook behind the per-half timings: with the merge in a
+    second launch, f4_launch = 1 launches the split kernel alone and
+    f4_launch = 2 the merge alone; run one after the other on one workspace
+    they give bitwise the output of the two-launch call, and each reports a
+    single launch."""
+    print(f"[f4-halves] L={L}", flush=True)
+    q, K, V = f4_inputs(1, 32, 8, L, 4200 + L)
+    qd, Kd, Vd = q.cuda(), K.cuda(), V.cuda()
+    S = ops.f4_default_splits(1, 8, L)
+    ws = torch.zeros(ops.load_library().db_f4_workspace_bytes(1, 32, 8, L, 128, S),
+                     dtype=torch.uint8, device="cuda")
+    try:
+        ops.tune("f4_merge", 2)
+        S_run = ops.f4_launch_info(1, 32, 8, L, S)[0]
+        assert ops.f4_launch_info(1, 32, 8, L, S) == (S_run, 2)
+        want = ops.f4_flashdecode(qd, Kd, Vd, workspace=ws)
+        torch.cuda.synchronize()
+        ws.zero_()
+        ops.tune("f4_launch", 1)
+        assert ops.f4_launch_info(1, 32, 8, L, S) == (S_run, 1)
+        ops.f4_flashdecode(qd, Kd, Vd, workspace=ws)
+        ops.tune("f4_launch", 2)
+        assert ops.f4_launch_info(1, 32, 8, L, S) == (S_run, 1)
+        got = ops.f4_flashdecode(qd, Kd, Vd, workspace=ws)
+        torch.cuda.synchronize()
+    finally:
+        ops.tune("f4_launch", 0)
+        ops.tune("f4_merge", 0)
+    assert torch.equal(got, want)
+    exact = cref.attention(q.numpy(), K.numpy(), V.numpy())
+    assert rel_l2(want.float().cpu().numpy(), exact) < F4_REL_L2
+
+
 @pytest.mark.parametrize("B,L", [(1, 1024), (1, 8192), (4, 8192), (8, 300)])
 def test_f4_in_launch_merge_matches_two_launch_merge(B, L):
     """The split merge done by the last split's workgroup (the default on an
