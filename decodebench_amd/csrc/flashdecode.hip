@@ -503,7 +503,9 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
   // it, with no LDS and no barrier.  Measured on MI355X against the grouped
   // merge below (interleaved runs, us): batch 1 L = 1024 (8 splits) 6.60 ->
   // 5.88, batch 4 L = 8192 23.9 -> 23.1, batch 8 L = 1024 9.9 -> 9.2, batch 4
-  // L = 32768 78.2 -> 77.5.
+  // L = 32768 78.2 -> 77.5.  (Two waves merge here, and the shuffled (m, l)
+  // loads of the grouped merge below only add latency: +0.05-0.07 us at
+  // batch 1 L = 1024, batch 4 L = 8192 and batch 8 L = 1024.)
   if (a.S <= kMergeChunk) {
     constexpr int kSlots = G * kD / 4;
     static_assert(kSlots <= kThreads, "one thread per slot");
@@ -545,11 +547,18 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
   } else
   // More splits: thread (grp, slot) owns float4 slot `slot` of the G x D outputs and the
   // splits grp, grp + kGrp, ...; the loads of a chunk of 8 splits are issued
-  // at once (16- and 8-byte buffer loads that miss the vector L1 and hit the
-  // XCD's L2), so S <= 8 kGrp costs one round trip; the split groups then
-  // meet in LDS.  (Split groups as adjacent lanes merged by lane exchanges
-  // instead, with four splits per load instruction, measured 1 us slower at
-  // batch 1, L = 8192 and 32768.)
+  // at once (16-byte buffer loads that miss the vector L1 and hit the XCD's
+  // L2), so S <= 8 kGrp costs one round trip; the split groups then meet in
+  // LDS.  The chunk's (m, l) pairs come in one 8-byte load per lane (lane j
+  // of a half-wave, whose lanes share one head and group, loads split j) and
+  // reach the other lanes by shuffles.  Here the merging CU's load
+  // instructions, not its bytes, set the pace: eight (m, l) loads per thread
+  // beside the eight record loads measured 0.2 us slower (batch 1, L = 8192
+  // 9.67 against 9.48 us, L = 32768 23.4 against 23.2), while records of
+  // half the bytes in as many instructions had gained nothing.  (Split
+  // groups as adjacent lanes merged by lane exchanges instead, with four
+  // splits per load instruction, measured 1 us slower at batch 1, L = 8192
+  // and 32768.)
   {
     constexpr int kSlots = G * kD / 4;
     constexpr int kGrp = kThreads / kSlots;  // >= 1: kThreads >= 256 >= kSlots
@@ -568,15 +577,21 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
     for (int s0 = grp; s0 < a.S; s0 += 8 * kGrp) {
       f4 ov[8];
       float2 mv[8];
+      const float2 mls = __builtin_bit_cast(
+          float2, __builtin_amdgcn_raw_buffer_load_b64(
+                      r_ml, (h * a.S + s0 + (lane & 7) * kGrp) * 8, 0, kSc1));
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         // splits past S read zero bytes (out of the buffer's range)
         const int sj = s0 + j * kGrp;
         ov[j] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(
                                            r_op, ((sj * G + h) * kD + 4 * d4) * 4, 0, kSc1));
-        mv[j] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
-                                               r_ml, (h * a.S + sj) * 8, 0, kSc1));
-        if (sj >= a.S) mv[j].x = kNegInf;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        mv[j].x = __shfl(mls.x, (lane & 32) + j);
+        mv[j].y = __shfl(mls.y, (lane & 32) + j);
+        if (s0 + j * kGrp >= a.S) mv[j].x = kNegInf;
       }
       float Mn = M;
 #pragma unroll
