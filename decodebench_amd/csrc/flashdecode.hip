@@ -136,8 +136,10 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
   __shared__ __align__(16) _Float16 s_v[NW][kTile][kVStride];
   static_assert(sizeof(float) * G * kD <= sizeof(s_v[0]), "wave outputs fit a V tile");
   auto s_o = [&](int w, int h) { return reinterpret_cast<float*>(&s_v[w][0][0]) + h * kD; };
-  __shared__ float s_m[NW][G];
-  __shared__ float s_l[NW][G];
+  // Per head, the running max and exp-sum of every wave: a head's NW values
+  // are contiguous, so the workgroup merge reads them in 16-byte loads.
+  __shared__ __align__(16) float s_m[G][NW];
+  __shared__ __align__(16) float s_l[G][NW];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
@@ -404,8 +406,8 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
     float l_tot = l_run + xor_lanes(l_run, 16);
     l_tot += xor_lanes(l_tot, 32);
     if (lane < G) {
-      s_m[wave][lane] = m_run;
-      s_l[wave][lane] = l_tot;
+      s_m[lane][wave] = m_run;
+      s_l[lane][wave] = l_tot;
     }
     if (n16 < G) {
 #pragma unroll
@@ -421,23 +423,34 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
     // launch otherwise.  (fp16 records of o_s / l_s, half the bytes, measured
     // 0.45 us slower per call at batch 1, L = 8192 and 32768, with the merge
     // in a second launch.)
-    for (int idx = threadIdx.x; idx < G * kD; idx += kThreads) {
-      const int h = idx / kD, d = idx % kD;
+    // One thread per float4 slot of the G x D outputs: 16-byte LDS reads and
+    // one 16-byte store per thread, a quarter of the instructions of one
+    // thread per output (bitwise the same results; measured on MI355X,
+    // interleaved, us: batch 1 L = 1024 5.55 -> 5.47, L = 8192 9.58 -> 9.45,
+    // L = 32768 23.30 -> 23.22, batch 4 L = 8192 22.87 -> 22.80, batch 8
+    // L = 1024 8.91 -> 8.82).
+    for (int idx = threadIdx.x; idx < G * kD / 4; idx += kThreads) {
+      const int h = idx / (kD / 4), d4 = idx % (kD / 4);
       float M = kNegInf;
 #pragma unroll
-      for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][h]);
-      float ow = 0.0f, lw = 0.0f;
+      for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[h][w]);
+      f4 ow = {0.0f, 0.0f, 0.0f, 0.0f};
+      float lw = 0.0f;
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
-        const float e = weight2(s_m[w][h], M);
-        ow += e * s_o(w, h)[d];
-        lw += e * s_l[w][h];
+        const float e = weight2(s_m[h][w], M);
+        ow += e * *reinterpret_cast<const f4*>(s_o(w, h) + 4 * d4);
+        lw += e * s_l[h][w];
       }
       if (a.S == 1) {
-        a.o[q_base + (size_t)h * kD + d] = to_h(ow / lw);
+        uint2 packed;
+        packed.x = pack_h2(ow[0] / lw, ow[1] / lw);
+        packed.y = pack_h2(ow[2] / lw, ow[3] / lw);
+        *reinterpret_cast<uint2*>(a.o + q_base + (size_t)h * kD + (size_t)d4 * 4) = packed;
       } else {
-        a.opart[(((size_t)pair * a.S + split) * G + h) * kD + d] = ow;
-        if (d == 0) a.ml[((size_t)pair * G + h) * a.S + split] = make_float2(M, lw);
+        *reinterpret_cast<f4*>(a.opart + (((size_t)pair * a.S + split) * G + h) * kD +
+                               (size_t)d4 * 4) = ow;
+        if (d4 == 0) a.ml[((size_t)pair * G + h) * a.S + split] = make_float2(M, lw);
       }
     }
   };  // run_split
