@@ -857,6 +857,37 @@ def test_f4_in_launch_merge_matches_two_launch_merge(B, L):
     assert rel_l2(one.float().cpu().numpy(), exact) < F4_REL_L2
 
 
+@pytest.mark.parametrize("Hq,L,S", [(64, 4096, 16), (16, 4096, 16), (8, 4096, 32), (8, 8192, 48),
+                                    (32, 8192, 20), (32, 8192, 40)])
+def test_f4_in_launch_grouped_merge_head_groups(Hq, L, S):
+    """The in-launch merge of more than 8 splits (split groups meeting in
+    LDS, the (m, l) pairs handed between the lanes of each half-wave) at
+    every query-head group size G = Hq / 8: G = 8, 2 and 1 lay out the
+    output slots over the half-waves differently from G = 4 (G = 1 puts two
+    split groups in one wave), and 20, 40 and 48 splits leave the last chunk
+    of a group partly past S.  Checked against the second-launch merge and
+    the fp64 oracle."""
+    print(f"[f4-grouped] Hq={Hq} L={L} S={S}", flush=True)
+    q, K, V = f4_inputs(1, Hq, 8, L, 5100 + Hq + L + S)
+    qd, Kd, Vd = q.cuda(), K.cuda(), V.cuda()
+    S_run, launches = ops.f4_launch_info(1, Hq, 8, L, S)
+    assert S_run > 8 and launches == 1       # merged in the first launch, grouped
+    one = ops.f4_flashdecode(qd, Kd, Vd, n_splits=S)
+    torch.cuda.synchronize()
+    lib = ops.load_library()
+    try:
+        assert lib.db_tune(b"f4_merge", 2) == 0
+        assert ops.f4_launch_info(1, Hq, 8, L, S) == (S_run, 2)
+        two = ops.f4_flashdecode(qd, Kd, Vd, n_splits=S)
+        torch.cuda.synchronize()
+    finally:
+        assert lib.db_tune(b"f4_merge", 0) == 0
+    assert rel_l2(one.float().cpu().numpy(), two.float().cpu().numpy()) < 1e-3
+    ref = stages.f4(q, K, V)
+    exact = cref.attention(q.numpy(), K.numpy(), V.numpy())
+    assert_parity(one, ref, exact, F4_REL_L2, f"f4 grouped Hq={Hq} L={L} S={S}")
+
+
 @pytest.mark.parametrize("B,L,k", [(1, 8192, 1), (1, 8192, 2), (1, 8192, 7), (4, 1024, 3),
                                    (8, 300, 2), (1, 32768, 5)])
 def test_f4_misplaced_splits_are_recomputed_by_the_merger(B, L, k):
