@@ -858,7 +858,10 @@ def test_f4_in_launch_merge_matches_two_launch_merge(B, L):
 
 
 @pytest.mark.parametrize("Hq,L,S", [(64, 4096, 16), (16, 4096, 16), (8, 4096, 32), (8, 8192, 48),
-                                    (32, 8192, 20), (32, 8192, 40)])
+                                    (32, 8192, 20), (32, 8192, 40),
+                                    # 4 tiles per split: 4-wave workgroups, so G = 8 has one
+                                    # split group and G = 1 eight
+                                    (64, 1024, 16), (32, 1024, 16), (8, 1024, 16)])
 def test_f4_in_launch_grouped_merge_head_groups(Hq, L, S):
     """The in-launch merge of more than 8 splits (split groups meeting in
     LDS, the (m, l) pairs handed between the lanes of each half-wave) at
