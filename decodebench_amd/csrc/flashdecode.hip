@@ -590,6 +590,9 @@ __global__ __launch_bounds__(NW * kWave) void f4_kernel(F4Args a) {
     for (int s0 = grp; s0 < a.S; s0 += 8 * kGrp) {
       f4 ov[8];
       float2 mv[8];
+      // (m, l) of split s0 + (lane & 7) kGrp of this lane's head; a split past
+      // S reads the next head's entry or zero bytes, and its m is set to -inf
+      // below.
       const float2 mls = __builtin_bit_cast(
           float2, __builtin_amdgcn_raw_buffer_load_b64(
                       r_ml, (h * a.S + s0 + (lane & 7) * kGrp) * 8, 0, kSc1));
