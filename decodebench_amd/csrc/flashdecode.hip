@@ -836,11 +836,13 @@ hipError_t launch_f4(const void* q, const void* k, const void* v, void* o,
   a.misplace_every = tuning().f4_misplace;
   a.scale_log2 = scale * kLog2e;
   (void)D;
-  // 8 waves where a split holds at least 16 tiles and either there are at
-  // most 8 (batch, kv-head) pairs (batch 1) or the 8 waves walk 2 tiles each
-  // (whole-line loads); 4 waves otherwise, which at larger batches stream
-  // long splits in the plain layout.  Measured on MI355X (32 q / 8 kv heads,
-  // interleaved, us, 4 / 8 waves):
+  // With at most 8 (batch, kv-head) pairs (batch 1): 8 waves where a split
+  // holds at least 16 tiles or there are at least 32 splits (whose merge
+  // takes 8 waves to split its loads); with more pairs, 8 waves only where
+  // they walk 2 tiles each (16 tiles per split, whole-line loads).  4 waves
+  // otherwise, which at larger batches stream long splits in the plain
+  // layout.  Measured on MI355X (32 q / 8 kv heads, interleaved, us, 4 / 8
+  // waves):
   //   batch 1: L = 1024 5.32 / 5.48, 2048 6.09 / 6.54, 4096 7.59 / 7.50,
   //            8192 9.67 / 9.47, 16384 14.42 / 14.07, 32768 23.47 / 23.22
   //   batch 2: L = 8192 14.06 / 14.50, 32768 41.33 / 42.10
@@ -848,7 +850,8 @@ hipError_t launch_f4(const void* q, const void* k, const void* v, void* o,
   //            8192 22.60 / 22.80, 32768 77.09 / 77.69
   //   batch 8: L = 1024 9.03 / 8.88, 2048 13.68 / 13.71, 4096 22.60 / 22.74,
   //            8192 40.83 / 40.98, 32768 150.5 / 152.1
-  const int auto_waves = a.tps >= 16 && (pairs <= 8 || a.tps <= 16) ? 8 : 4;
+  const int auto_waves =
+      pairs <= 8 ? (a.tps >= 16 || a.S >= 32 ? 8 : 4) : (a.tps == 16 ? 8 : 4);
   int waves = tuning().f4_waves > 0 ? tuning().f4_waves : auto_waves;
   // Whole-line K loads when a wave walks at most 2 tiles or there are at
   // most 8 (batch, kv-head) pairs; the plain layout streams long splits of
